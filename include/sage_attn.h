@@ -1,0 +1,122 @@
+/*
+ * sage_attn.h — C ABI of the MI355X (gfx950) SageAttention hot path.
+ *
+ * The library replaces the two device stages of TriBench's
+ * kernels/sage_attn/triton_impl.py:
+ *
+ *   sage_prepass()  <- per_block_int8()              triton_impl.py:35-82
+ *                      quant_per_block_int8_kernel() triton_impl.py:7-33
+ *                      (+ the K channel-mean hook     triton_impl.py:39-40,
+ *                         + FP8 V, which the reference does not have)
+ *   sage_attn_fwd() <- _attn_fwd[grid](...) launch    triton_impl.py:186-199
+ *                      _attn_fwd / _attn_fwd_inner    triton_impl.py:86-160
+ *
+ * The Python entry point that strings them together (the counterpart of
+ * run_sage_attn, triton_impl.py:162-200) lives in
+ * tribench_amd/kernels/sage_attn/hip_impl.py and binds this header with ctypes.
+ *
+ * Conventions
+ *  - Every tensor is described by a base pointer, its logical sizes and the
+ *    element strides of its batch, head and sequence dimensions (3 values,
+ *    in that order).  The head-dim stride must be 1.  Row starts must be
+ *    16-byte aligned.  This covers both of the reference's layouts
+ *    ("HND" and "NHD", triton_impl.py:42-55).
+ *  - The caller owns every device buffer.  The library never allocates or
+ *    frees device memory and keeps no pointer after a call returns.
+ *  - Every call is asynchronous on `stream` (a hipStream_t; NULL means the
+ *    default stream) and returns 0 on success.  A non-zero status leaves a
+ *    message in sage_last_error(); argument errors contain the words
+ *    "invalid argument".
+ *  - Head dims 64 and 128 are supported.
+ */
+#ifndef SAGE_ATTN_H
+#define SAGE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SAGE_ABI_VERSION 1
+
+/* element types (dtype codes used by every entry point) */
+#define SAGE_DTYPE_F32 0
+#define SAGE_DTYPE_F16 1
+#define SAGE_DTYPE_BF16 2
+#define SAGE_DTYPE_FP8E4M3 3 /* OCP e4m3 ("e4m3fn"), bias 7, max 448 */
+
+/* v_mode of sage_prepass */
+#define SAGE_V_NONE 0 /* V is not touched by the pre-pass */
+#define SAGE_V_FP8 1  /* per-channel FP8 e4m3 V: v8 = RNE_sat(v / v_scale[c]) */
+
+/* pv_mode of sage_attn_fwd: the operand type of the P.V product */
+#define SAGE_PV_F16 0  /* P and V rounded to fp16 (the reference's choice, triton_impl.py:112-113,189) */
+#define SAGE_PV_BF16 1 /* P and V in bf16 */
+#define SAGE_PV_FP8 2  /* P and V in FP8 e4m3; V comes from sage_prepass(v_mode=SAGE_V_FP8) */
+
+/* Library version; bumped whenever a signature below changes. */
+int sage_abi_version(void);
+
+/* Message of the last failed call on the calling thread ("" if none). */
+const char* sage_last_error(void);
+
+/* Bytes of scratch that sage_prepass needs for the given problem
+ * (the per-chunk K channel sums and V channel maxima). */
+size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t D, int smooth_k,
+                                    int v_mode);
+
+/*
+ * Pre-pass: INT8 per-block quantization of Q and K with fp32 scales.
+ * Replaces per_block_int8() (triton_impl.py:35-82).
+ *
+ *  q [B,Hq,Nq,D], k [B,Hkv,Nkv,D], v [B,Hkv,Nkv,D]   in_dtype (F32/F16/BF16)
+ *  q_mul     fp32 multiplier folded into Q before quantization; the
+ *            reference passes fp32(sm_scale * 1.44269504) (triton_impl.py:69)
+ *  blkq/blkk rows per scale block (reference: 128 / 64); 16 <= blk <= 256,
+ *            multiples of 16
+ *  q_sub     rows per Q scale: blkq (one scale per block, the reference) or a
+ *            divisor of blkq that is a multiple of 16 (per-wave scales)
+ *  smooth_k  1: km[c] = mean over tokens of k[..,c] (fp32, fixed reduction
+ *            order), K is quantized as fp32(k) - km[c]
+ *  outputs   q8 [B,Hq,Nq,D] int8 + q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)]
+ *            k8 [B,Hkv,Nkv,D] int8 + k_scale [B,Hkv,ceil(Nkv/blkk)]
+ *            km [B,Hkv,D] fp32 (written when smooth_k; may be NULL otherwise)
+ *            v8 [B,Hkv,Nkv,D] e4m3 bytes + v_scale [B,Hkv,D] (v_mode FP8)
+ *  q8/k8/v8 strides are given like the input strides; scales, km and
+ *  v_scale are dense.
+ */
+int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int64_t B, int64_t Hq,
+                 int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, const int64_t* q_strides,
+                 const int64_t* k_strides, const int64_t* v_strides, float q_mul, int blkq,
+                 int blkk, int q_sub, int smooth_k, int v_mode, int8_t* q8,
+                 const int64_t* q8_strides, float* q_scale, int8_t* k8, const int64_t* k8_strides,
+                 float* k_scale, float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Fused attention: O = softmax2(dequant(Q8 K8^T)) V with an online,
+ * base-2 softmax (the log2(e) factor is already folded into q_scale).
+ * Replaces the _attn_fwd launch (triton_impl.py:186-199).
+ *
+ *  q8/q_scale/k8/k_scale  as written by sage_prepass (same blkq, q_sub, blkk)
+ *  v      [B,Hkv,Nkv,D] in v_dtype (F32/F16/BF16, or FP8E4M3 with v_scale)
+ *  o      [B,Hq,Nq,D] in o_dtype (F32/F16/BF16)
+ *  causal 1: key j is visible to query i iff j <= i (top-left aligned, the
+ *         torch.tril mask of reference.py:19-22)
+ *  GQA    query head h reads KV head h / (Hq/Hkv) (triton_impl.py:137,145,147)
+ *  blkk must be a multiple of 64, q_sub a multiple of 16.
+ */
+int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_scale,
+                  const int8_t* k8, const int64_t* k8_strides, const float* k_scale,
+                  const void* v, int v_dtype, const int64_t* v_strides, const float* v_scale,
+                  void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
+                  int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq, int blkk,
+                  int q_sub, int pv_mode, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SAGE_ATTN_H */

@@ -1,0 +1,136 @@
+"""GPU parity of the HIP pre-pass against the CPU oracle: bit-exact.
+
+INT8 Q/K, the fp32 block scales, the K channel mean and FP8 V must equal the
+oracle's values bit for bit (the reference's quantization,
+triton_impl.py:7-82, restated in oracle/sage_oracle.py).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sage_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp32": torch.float32, "fp16": torch.float16, "bf16": torch.bfloat16}
+
+# (B, Hq, Hkv, N, D, dtype, q_sub, smooth_k, v_fp8, k_offset_std, v_dist)
+CASES = [
+    (1, 2, 2, 256, 64, "fp32", 128, True, False, 2.0, "normal"),      # config 1 shape
+    (1, 2, 2, 256, 64, "fp32", 128, False, False, 2.0, "normal"),     # reference semantics (no smoothing)
+    (2, 4, 2, 300, 128, "bf16", 128, True, False, 2.0, "normal"),     # ragged tail, GQA
+    (1, 3, 3, 1000, 64, "fp16", 32, True, False, 4.0, "normal"),      # per-wave Q scales
+    (2, 6, 1, 777, 128, "bf16", 32, True, True, 2.0, "student_t"),    # FP8 V, GQA 6:1
+    (1, 4, 4, 4096, 128, "bf16", 128, True, False, 2.0, "normal"),    # 16 K-stat chunks
+    (1, 2, 2, 17776, 64, "bf16", 128, True, True, 2.0, "normal"),     # config-4 length, 14 chunks
+]
+
+
+def _ids(c):
+    return f"B{c[0]}Hq{c[1]}Hkv{c[2]}N{c[3]}D{c[4]}-{c[5]}-qsub{c[6]}-smooth{int(c[7])}-fp8v{int(c[8])}"
+
+
+def _inputs(pack_ref, B, Hq, Hkv, N, D, dtype, off, vdist, seed=0):
+    case = dict(batch_size=B, num_heads=Hq, num_kv_heads=Hkv, seq_len=N, head_dim=D,
+                k_offset_std=off, v_dist=vdist, v_df=3)
+    return pack_ref.make_inputs(case, "cpu", seed, DT[dtype])
+
+
+def _np32(t):
+    return t.float().cpu().numpy()
+
+
+def _eq_bits(a, b):
+    a = np.asarray(a)
+    b = np.asarray(b)
+    assert a.shape == b.shape, (a.shape, b.shape)
+    if a.dtype == np.float32:
+        # identical values; +0.0 and -0.0 count as equal
+        return bool(np.array_equal(a, b))
+    return bool(np.array_equal(a, b))
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_ids(c) for c in CASES])
+def test_prepass_bitexact(case, pack_ref, hip_impl, gpu_device):
+    B, Hq, Hkv, N, D, dtype, q_sub, smooth, vfp8, off, vdist = case
+    print(f"[prepass] {_ids(case)}", flush=True)
+    inp = _inputs(pack_ref, B, Hq, Hkv, N, D, dtype, off, vdist)
+    want = O.prepass(_np32(inp["q"]), _np32(inp["k"]), _np32(inp["v"]), q_sub=q_sub, smooth_k=smooth,
+                     v_fp8=vfp8)
+    got = hip_impl.prepass(inp["q"].to(gpu_device), inp["k"].to(gpu_device), inp["v"].to(gpu_device),
+                           q_sub=q_sub, smooth_k=smooth, v_fp8=vfp8)
+    torch.cuda.synchronize()
+    keys = ["q8", "q_scale", "k8", "k_scale"] + (["km"] if smooth else []) + (["v8", "v_scale"] if vfp8 else [])
+    for key in keys:
+        g = got[key].cpu().numpy()
+        w = want[key]
+        if not _eq_bits(g, w):
+            diff = np.argwhere(g != w)
+            raise AssertionError(f"{key}: {len(diff)} mismatches, first at {diff[:3].tolist()}: "
+                                 f"got {g[tuple(diff[0])]} want {w[tuple(diff[0])]}")
+
+
+def test_prepass_nhd_layout(pack_ref, hip_impl, gpu_device):
+    """The reference's NHD layout (triton_impl.py:49-55) through strides."""
+    inp = _inputs(pack_ref, 2, 4, 4, 200, 64, "bf16", 2.0, "normal")
+    q = inp["q"].transpose(1, 2).contiguous()  # [B, N, H, D]
+    k = inp["k"].transpose(1, 2).contiguous()
+    want = O.prepass(_np32(inp["q"]), _np32(inp["k"]), smooth_k=True)
+    got = hip_impl.prepass(q.to(gpu_device), k.to(gpu_device), k.to(gpu_device), smooth_k=True,
+                           tensor_layout="NHD")
+    torch.cuda.synchronize()
+    assert tuple(got["q8"].shape) == tuple(q.shape)
+    assert np.array_equal(got["q8"].cpu().transpose(1, 2).numpy(), want["q8"])
+    assert np.array_equal(got["k8"].cpu().transpose(1, 2).numpy(), want["k8"])
+    assert np.array_equal(got["q_scale"].cpu().numpy(), want["q_scale"])
+    assert np.array_equal(got["k_scale"].cpu().numpy(), want["k_scale"])
+    assert np.array_equal(got["km"].cpu().numpy(), want["km"])
+
+
+def test_per_block_int8_mirror(pack_ref, hip_impl, gpu_device):
+    """per_block_int8(q, k, km) semantics: k - km in k's dtype, then quantize."""
+    inp = _inputs(pack_ref, 1, 2, 2, 333, 128, "fp16", 2.0, "normal")
+    q, k = inp["q"].to(gpu_device), inp["k"].to(gpu_device)
+    km = k.float().mean(dim=2, keepdim=True).to(k.dtype)
+    q8, qs, k8, ks = hip_impl.per_block_int8(q, k, km=km)
+    torch.cuda.synchronize()
+    k_s = (k - km).float().cpu().numpy()
+    wq8, wqs = O.quant_per_block_int8(_np32(q), 128, mul=O.q_multiplier(128))
+    wk8, wks = O.quant_per_block_int8(k_s, 64)
+    assert np.array_equal(q8.cpu().numpy(), wq8) and np.array_equal(qs.cpu().numpy(), wqs)
+    assert np.array_equal(k8.cpu().numpy(), wk8) and np.array_equal(ks.cpu().numpy(), wks)
+
+
+def test_prepass_special_blocks(hip_impl, gpu_device):
+    """All-zero block, exact ties, the 0x3EFFFFFF quirk, -0.0, tiny values."""
+    D = 64
+    N = 256
+    k = torch.zeros((1, 1, N, D), dtype=torch.float32)
+    # block 0 all zero; block 1 has amax 127 so scale is exactly 1.0
+    blk1 = k[0, 0, 64:128]
+    blk1[0, 0] = 127.0
+    blk1[0, 1] = 0.5
+    blk1[0, 2] = -0.5
+    blk1[0, 3] = 1.5
+    blk1[0, 4] = -2.5
+    blk1[0, 5] = float(np.uint32(0x3EFFFFFF).view(np.float32))
+    blk1[0, 6] = -float(np.uint32(0x3EFFFFFF).view(np.float32))
+    blk1[0, 7] = -0.0
+    blk1[0, 8] = 1e-30
+    blk1[0, 9] = -126.5
+    # block 2: tiny values (scale near the fast-division limit)
+    k[0, 0, 128:192] = torch.randn((64, D)) * 1e-33
+    # block 3: large values
+    k[0, 0, 192:256] = torch.randn((64, D)) * 1e30
+    q = k.clone()
+    got = hip_impl.prepass(q.to(gpu_device), k.to(gpu_device), k.to(gpu_device), smooth_k=False)
+    torch.cuda.synchronize()
+    wk8, wks = O.quant_per_block_int8(k.numpy(), 64)
+    gk8 = got["k8"].cpu().numpy()
+    assert np.array_equal(got["k_scale"].cpu().numpy(), wks)
+    assert np.array_equal(gk8, wk8)
+    assert wks[0, 0, 0] == 0.0 and wks[0, 0, 1] == 1.0
+    row = gk8[0, 0, 64]
+    assert list(row[:10]) == [127, 1, -1, 2, -3, 1, -1, 0, 0, -127]

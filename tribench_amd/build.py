@@ -1,0 +1,97 @@
+"""Build the gfx950 C-ABI library ``tribench_amd/lib/libsage_attn.so``.
+
+Every ``csrc/*.hip`` translation unit is compiled with ``hipcc
+--offload-arch=gfx950`` and linked into one shared library.  Builds in-tree
+(the ``.so`` travels with the source tree) and always recompiles.
+
+Usage: ``python -m tribench_amd.build [-j N]``.
+"""
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+LIBDIR = PKG / "lib"
+LIB = LIBDIR / "libsage_attn.so"
+ARCH = "gfx950"
+
+# Common flags.  Packed-FP32 instructions are disabled for all device code.
+COMMON = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    f"-I{PKG.parent / 'include'}",
+]
+# Per-unit flags.  The pre-pass must round exactly like the reference, so no
+# contraction of multiplies and adds into FMAs there.
+UNIT_FLAGS = {
+    "sage_prepass.hip": ["-ffp-contract=off"],
+    "sage_attn_fwd.hip": [],
+    "sage_abi.hip": [],
+}
+
+
+def hipcc() -> str:
+    exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(exe).exists():
+        raise RuntimeError("hipcc not found (ROCm is required to build the HIP library)")
+    return exe
+
+
+def _compile(src: Path, obj: Path) -> None:
+    cmd = [hipcc(), *COMMON, *UNIT_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    # hipcc's host pass warns about the device-only target feature; drop that noise
+    noise = ("packed-fp32-ops", "not a recognized feature")
+    msgs = [ln for ln in res.stderr.splitlines() if ln.strip() and not any(x in ln for x in noise)]
+    if msgs:
+        print("\n".join(msgs), file=sys.stderr)
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> Path:
+    """Compile every HIP unit for gfx950 and link ``libsage_attn.so``."""
+    srcs = sorted(CSRC.glob("*.hip"))
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    objdir = PKG / "_build"
+    objdir.mkdir(exist_ok=True)
+    LIBDIR.mkdir(exist_ok=True)
+    objs = [objdir / (s.stem + ".o") for s in srcs]
+    jobs = jobs or min(len(srcs), os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for f in [ex.submit(_compile, s, o) for s, o in zip(srcs, objs)]:
+            f.result()
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+def main(argv: list[str] | None = None) -> int:
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("-j", "--jobs", type=int, default=None)
+    args = p.parse_args(argv)
+    build(args.jobs)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

@@ -1,0 +1,455 @@
+// sage_prepass.hip — HBM-bound pre-pass of the SageAttention hot path.
+//
+// Replaces per_block_int8() / quant_per_block_int8_kernel()
+// (kernels/sage_attn/triton_impl.py:7-82) and adds what the reference only
+// hooks (K smoothing, triton_impl.py:39-40) or lacks (per-channel FP8 V).
+//
+// Two launches:
+//   A  (one grid, roles by block index)
+//        K statistics:  per (chunk, kv-head, batch) fp32 channel sums of K
+//                       (and channel max|v| for FP8 V) in a fixed order
+//        Q quant:       per (128-row block, head, batch) INT8 + scale(s)
+//        K quant:       here as well when no K statistics are needed
+//   B  K quant with the channel mean subtracted (+ FP8 V quant)
+//
+// Every block is 256 threads.  A block's data is read once from HBM with
+// 16-byte loads, held in registers while the block's max|x| is reduced, then
+// quantized and written with 16-byte stores.  Build with -ffp-contract=off:
+// the element arithmetic must round exactly like the reference's.
+#include "sage_device.h"
+
+namespace sage {
+
+constexpr int kPrepassThreads = 256;
+
+struct PrepassArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t B, Hq, Hkv, Nq, Nkv;
+  int64_t sq[3], sk[3], sv[3];     // input strides (batch, head, seq)
+  int64_t sq8[3], sk8[3], sv8[3];  // output strides
+  float q_mul;
+  int blkq, blkk, q_sub;
+  int smooth_k, v_fp8;
+  int8_t* q8;
+  float* q_scale;
+  int8_t* k8;
+  float* k_scale;
+  float* km;
+  uint8_t* v8;
+  float* v_scale;
+  float* psum;   // [B, Hkv, nch, D] K channel sums per chunk
+  float* pamax;  // [B, Hkv, nch, D] V channel max|v| per chunk
+  int64_t nch, chunk;
+  int64_t nqb, nkb;  // blocks per head
+  int64_t n_stat, n_qblk, n_kblk_a;  // role counts of launch A
+};
+
+// ---------------------------------------------------------------------------
+// One quantization block: rows [0, rows_valid) of BLK rows x D, scale per
+// q_sub rows (q_sub == BLK: one scale per block, triton_impl.py:28,33).
+// x = fp32(in) * mul (if use_mul) - km[c] (if km); tail rows count as 0.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
+                            int q_sub, bool use_mul, float mul, const float* km_s,
+                            int8_t* __restrict__ dst, int64_t dn, float* __restrict__ scale_dst,
+                            uint32_t* amax_s, float* scl_s, float* rcp_s) {
+  constexpr int CPR = D / 16;   // 16-element items per row
+  constexpr int MAXJ = D / 16;  // items per thread when blk == 256
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int nit = blk * CPR;  // a multiple of 64: whole waves are valid or not
+  const int nsub = blk / q_sub;
+
+  if (tid < 16) amax_s[tid] = 0u;
+  __syncthreads();
+
+  Raw8<T> raw[MAXJ][2];
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int it = tid + kPrepassThreads * j;
+    if (it - lane >= nit) break;  // wave-uniform
+    const int row = it / CPR, c = it % CPR;
+    if (row < rows_valid) {
+      const T* p = src + (int64_t)row * sn + c * 16;
+      raw[j][0] = load8<T>(p);
+      raw[j][1] = load8<T>(p + 8);
+    } else {
+      raw[j][0] = zero8<T>();
+      raw[j][1] = zero8<T>();
+    }
+    float am = 0.0f;
+    if (row < rows_valid) {  // tail rows stay out of the block max
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float x = elem<T>(raw[j][e >> 3], e & 7);
+        if (use_mul) x = x * mul;
+        if (km_s) x = x - km_s[c * 16 + e];
+        am = fmaxf(am, fabsf(x));
+      }
+    }
+    am = wave_max(am);
+    // a wave's 64 items cover 64/CPR consecutive rows inside one sub-block
+    if (lane == 0) atomicMax(&amax_s[((it - lane) / CPR) / q_sub], __float_as_uint(am));
+  }
+  __syncthreads();
+  if (tid < nsub) {
+    const float sc = block_scale(__uint_as_float(amax_s[tid]));
+    scl_s[tid] = sc;
+    rcp_s[tid] = sc > 0.0f ? 1.0f / sc : 0.0f;
+    scale_dst[tid] = sc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < MAXJ; ++j) {
+    const int it = tid + kPrepassThreads * j;
+    if (it - lane >= nit) break;
+    const int row = it / CPR, c = it % CPR;
+    if (row >= rows_valid) continue;
+    const int sub = row / q_sub;
+    const float sc = scl_s[sub], rc = rcp_s[sub];
+    const bool fast = fast_div_ok(sc);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      float x = elem<T>(raw[j][e >> 3], e & 7);
+      if (use_mul) x = x * mul;
+      if (km_s) x = x - km_s[c * 16 + e];
+      const int8_t qv = quant_elem(x, sc, rc, fast);
+      w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// K statistics of one chunk [n0, n1): fp32 channel sums in the fixed order of
+// sage_quant_math.h, and (if vsrc) channel max|v|.
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__device__ void kstats_chunk(const T* __restrict__ ksrc, int64_t ksn, const T* __restrict__ vsrc,
+                             int64_t vsn, int64_t n0, int64_t n1, float* __restrict__ psum,
+                             float* __restrict__ pamax, float* red_s) {
+  constexpr int CG = D / 8;
+  constexpr int TL = kPrepassThreads / CG;
+  const int tid = threadIdx.x;
+  const int cg = tid % CG, tl = tid / CG;
+  float acc[8], vm[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    acc[e] = 0.0f;
+    vm[e] = 0.0f;
+  }
+  constexpr int U = 4;  // rows in flight per thread
+  for (int64_t nb = n0 + tl; nb < n1; nb += (int64_t)TL * U) {
+    Raw8<T> r[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t n = nb + (int64_t)u * TL;
+      r[u] = (n < n1) ? load8<T>(ksrc + n * ksn + cg * 8) : zero8<T>();
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (nb + (int64_t)u * TL < n1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = acc[e] + elem<T>(r[u], e);
+      }
+    }
+    if (vsrc) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t n = nb + (int64_t)u * TL;
+        r[u] = (n < n1) ? load8<T>(vsrc + n * vsn + cg * 8) : zero8<T>();
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vm[e] = fmaxf(vm[e], fabsf(elem<T>(r[u], e)));
+      }
+    }
+  }
+  // tree over the TL token lanes: acc[tl] += acc[tl + s], s = TL/2 .. 1
+  float* row = red_s + tl * D + cg * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) row[e] = acc[e];
+  __syncthreads();
+  for (int s = TL / 2; s >= 1; s >>= 1) {
+    if (tl < s) {
+      const float* o = red_s + (tl + s) * D + cg * 8;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) row[e] = row[e] + o[e];
+    }
+    __syncthreads();
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) psum[cg * 8 + e] = row[e];
+  }
+  if (vsrc) {
+    __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) row[e] = vm[e];
+    __syncthreads();
+    for (int s = TL / 2; s >= 1; s >>= 1) {
+      if (tl < s) {
+        const float* o = red_s + (tl + s) * D + cg * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) row[e] = fmaxf(row[e], o[e]);
+      }
+      __syncthreads();
+    }
+    if (tl == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pamax[cg * 8 + e] = row[e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// FP8 e4m3 V block: v8 = RNE_sat(v / v_scale[c]) (v_scale[c] == 0 -> 0)
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+__device__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
+                             const float* vs_s, uint8_t* __restrict__ dst, int64_t dn) {
+  constexpr int CPR = D / 16;
+  const int nit = blk * CPR;
+  for (int it = threadIdx.x; it < nit; it += kPrepassThreads) {
+    const int row = it / CPR, c = it % CPR;
+    if (row >= rows_valid) continue;
+    const T* p = src + (int64_t)row * sn + c * 16;
+    Raw8<T> r0 = load8<T>(p), r1 = load8<T>(p + 8);
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float x = elem<T>(e < 8 ? r0 : r1, e & 7);
+      const float s = vs_s[c * 16 + e];
+      const float t = s > 0.0f ? x / s : 0.0f;
+      w[e >> 2] |= ((uint32_t)f32_to_e4m3(t)) << (8 * (e & 3));
+    }
+    *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+template <typename T, int D>
+__device__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, float* scl_s,
+                             float* rcp_s) {
+  const int64_t qb = r % a.nqb, h = (r / a.nqb) % a.Hq, b = r / (a.nqb * a.Hq);
+  const int64_t row0 = qb * a.blkq;
+  const int rows_valid = (int)min<int64_t>(a.blkq, a.Nq - row0);
+  const T* src = static_cast<const T*>(a.q) + b * a.sq[0] + h * a.sq[1] + row0 * a.sq[2];
+  int8_t* dst = a.q8 + b * a.sq8[0] + h * a.sq8[1] + row0 * a.sq8[2];
+  const int nsub = a.blkq / a.q_sub;
+  float* sdst = a.q_scale + ((b * a.Hq + h) * a.nqb + qb) * nsub;
+  quant_block<T, D>(src, a.sq[2], rows_valid, a.blkq, a.q_sub, true, a.q_mul, nullptr, dst, a.sq8[2],
+                    sdst, amax_s, scl_s, rcp_s);
+}
+
+template <typename T, int D>
+__device__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s, uint32_t* amax_s,
+                             float* scl_s, float* rcp_s) {
+  const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
+  const int64_t row0 = kb * a.blkk;
+  const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
+  const T* src = static_cast<const T*>(a.k) + b * a.sk[0] + h * a.sk[1] + row0 * a.sk[2];
+  int8_t* dst = a.k8 + b * a.sk8[0] + h * a.sk8[1] + row0 * a.sk8[2];
+  float* sdst = a.k_scale + (b * a.Hkv + h) * a.nkb + kb;
+  quant_block<T, D>(src, a.sk[2], rows_valid, a.blkk, a.blkk, false, 1.0f, km_s, dst, a.sk8[2], sdst,
+                    amax_s, scl_s, rcp_s);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs a) {
+  __shared__ uint32_t amax_s[16];
+  __shared__ float scl_s[16], rcp_s[16];
+  __shared__ float red_s[kPrepassThreads / (D / 8) * D];
+  int64_t r = blockIdx.x;
+  if (r < a.n_stat) {
+    const int64_t c = r % a.nch, h = (r / a.nch) % a.Hkv, b = r / (a.nch * a.Hkv);
+    const int64_t n0 = c * a.chunk, n1 = min<int64_t>(n0 + a.chunk, a.Nkv);
+    const T* ks = static_cast<const T*>(a.k) + b * a.sk[0] + h * a.sk[1];
+    const T* vs = a.v_fp8 ? static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1] : nullptr;
+    const int64_t slot = ((b * a.Hkv + h) * a.nch + c) * D;
+    kstats_chunk<T, D>(ks, a.sk[2], vs, a.sv[2], n0, n1, a.psum + slot,
+                       a.v_fp8 ? a.pamax + slot : nullptr, red_s);
+    return;
+  }
+  r -= a.n_stat;
+  if (r < a.n_qblk) {
+    quant_q_role<T, D>(a, r, amax_s, scl_s, rcp_s);
+    return;
+  }
+  r -= a.n_qblk;
+  if (r < a.n_kblk_a) quant_k_role<T, D>(a, r, nullptr, amax_s, scl_s, rcp_s);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs a) {
+  __shared__ uint32_t amax_s[16];
+  __shared__ float scl_s[16], rcp_s[16];
+  __shared__ float km_s[D], vs_s[D];
+  const int64_t r = blockIdx.x;
+  const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
+  const int tid = threadIdx.x;
+  const int64_t base = (b * a.Hkv + h) * a.nch * D;
+  if (tid < D) {
+    if (a.smooth_k) {
+      float s = a.psum[base + tid];
+      for (int64_t c = 1; c < a.nch; ++c) s = s + a.psum[base + c * D + tid];
+      const float m = s / (float)a.Nkv;
+      km_s[tid] = m;
+      if (kb == 0) a.km[(b * a.Hkv + h) * D + tid] = m;
+    }
+    if (a.v_fp8) {
+      float m = a.pamax[base + tid];
+      for (int64_t c = 1; c < a.nch; ++c) m = fmaxf(m, a.pamax[base + c * D + tid]);
+      const float s = m / 448.0f;
+      vs_s[tid] = s;
+      if (kb == 0) a.v_scale[(b * a.Hkv + h) * D + tid] = s;
+    }
+  }
+  __syncthreads();
+  quant_k_role<T, D>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
+  if (a.v_fp8) {
+    const int64_t row0 = kb * a.blkk;
+    const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
+    const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1] + row0 * a.sv[2];
+    uint8_t* dst = a.v8 + b * a.sv8[0] + h * a.sv8[1] + row0 * a.sv8[2];
+    vquant_block<T, D>(src, a.sv[2], rows_valid, a.blkk, vs_s, dst, a.sv8[2]);
+  }
+}
+
+template <typename T, int D>
+static int launch_prepass(const PrepassArgs& a, hipStream_t st) {
+  const int64_t na = a.n_stat + a.n_qblk + a.n_kblk_a;
+  if (na > 0) {
+    hipLaunchKernelGGL((prepass_a_kernel<T, D>), dim3((unsigned)na), dim3(kPrepassThreads), 0, st, a);
+    if (int rc = check_launch("sage_prepass (launch A)")) return rc;
+  }
+  if (a.n_kblk_a == 0) {
+    const int64_t nb = a.nkb * a.Hkv * a.B;
+    hipLaunchKernelGGL((prepass_b_kernel<T, D>), dim3((unsigned)nb), dim3(kPrepassThreads), 0, st, a);
+    if (int rc = check_launch("sage_prepass (launch B)")) return rc;
+  }
+  return 0;
+}
+
+static bool strides_ok(const int64_t* s, int esize) {
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0 || (s[i] * esize) % 16 != 0) return false;
+  return true;
+}
+
+}  // namespace sage
+
+using namespace sage;
+
+extern "C" size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t D,
+                                               int smooth_k, int v_mode) {
+  if (B <= 0 || Hkv <= 0 || Nkv <= 0 || D <= 0) return 0;
+  const int64_t per = B * Hkv * kstat_num_chunks(Nkv) * D * (int64_t)sizeof(float);
+  size_t bytes = 0;
+  if (smooth_k) bytes += (size_t)per;
+  if (v_mode == SAGE_V_FP8) bytes += (size_t)per;
+  return bytes;
+}
+
+extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                            int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
+                            int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
+                            float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
+                            float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0)
+    return fail("sage_prepass: invalid argument: empty shape B=%lld Hq=%lld Hkv=%lld Nq=%lld Nkv=%lld",
+                (long long)B, (long long)Hq, (long long)Hkv, (long long)Nq, (long long)Nkv);
+  if (D != 64 && D != 128)
+    return fail("sage_prepass: invalid argument: head_dim %lld (supported: 64, 128)", (long long)D);
+  if (Hq % Hkv != 0)
+    return fail("sage_prepass: invalid argument: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq,
+                (long long)Hkv);
+  if (in_dtype != SAGE_DTYPE_F32 && in_dtype != SAGE_DTYPE_F16 && in_dtype != SAGE_DTYPE_BF16)
+    return fail("sage_prepass: invalid argument: in_dtype %d", in_dtype);
+  auto blk_ok = [](int b) { return b >= 16 && b <= 256 && b % 16 == 0; };
+  if (!blk_ok(blkq) || !blk_ok(blkk))
+    return fail("sage_prepass: invalid argument: blkq=%d blkk=%d (16..256, multiples of 16)", blkq, blkk);
+  if (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0 || blkq / q_sub > 16)
+    return fail("sage_prepass: invalid argument: q_sub=%d for blkq=%d", q_sub, blkq);
+  if (v_mode != SAGE_V_NONE && v_mode != SAGE_V_FP8)
+    return fail("sage_prepass: invalid argument: v_mode %d", v_mode);
+  const bool vfp8 = v_mode == SAGE_V_FP8;
+  if (!q || !k || !q8 || !k8 || !q_scale || !k_scale || !q_strides || !k_strides || !q8_strides ||
+      !k8_strides)
+    return fail("sage_prepass: invalid argument: null pointer");
+  if (smooth_k && !km) return fail("sage_prepass: invalid argument: km is null with smooth_k");
+  if (vfp8 && (!v || !v8 || !v_scale || !v_strides || !v8_strides))
+    return fail("sage_prepass: invalid argument: null V pointer with v_mode FP8");
+  const int es = in_dtype == SAGE_DTYPE_F32 ? 4 : 2;
+  if (!strides_ok(q_strides, es) || !strides_ok(k_strides, es) || !strides_ok(q8_strides, 1) ||
+      !strides_ok(k8_strides, 1) || (vfp8 && (!strides_ok(v_strides, es) || !strides_ok(v8_strides, 1))))
+    return fail("sage_prepass: invalid argument: strides must keep 16-byte aligned rows");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)(vfp8 ? v : nullptr) |
+       (uintptr_t)(vfp8 ? v8 : nullptr)) % 16 != 0)
+    return fail("sage_prepass: invalid argument: base pointers must be 16-byte aligned");
+  const size_t need = sage_prepass_workspace_bytes(B, Hkv, Nkv, D, smooth_k, v_mode);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail("sage_prepass: invalid argument: workspace %zu bytes < %zu", workspace_bytes, need);
+
+  PrepassArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.Nq = Nq;
+  a.Nkv = Nkv;
+  for (int i = 0; i < 3; ++i) {
+    a.sq[i] = q_strides[i];
+    a.sk[i] = k_strides[i];
+    a.sq8[i] = q8_strides[i];
+    a.sk8[i] = k8_strides[i];
+    a.sv[i] = vfp8 ? v_strides[i] : 0;
+    a.sv8[i] = vfp8 ? v8_strides[i] : 0;
+  }
+  a.q_mul = q_mul;
+  a.blkq = blkq;
+  a.blkk = blkk;
+  a.q_sub = q_sub;
+  a.smooth_k = smooth_k ? 1 : 0;
+  a.v_fp8 = vfp8 ? 1 : 0;
+  a.q8 = q8;
+  a.q_scale = q_scale;
+  a.k8 = k8;
+  a.k_scale = k_scale;
+  a.km = km;
+  a.v8 = v8;
+  a.v_scale = v_scale;
+  a.nch = kstat_num_chunks(Nkv);
+  a.chunk = kstat_chunk_tokens(Nkv);
+  const int64_t per = B * Hkv * a.nch * D;
+  float* ws = static_cast<float*>(workspace);
+  a.psum = smooth_k ? ws : nullptr;
+  a.pamax = vfp8 ? ws + (smooth_k ? per : 0) : nullptr;
+  a.nqb = (Nq + blkq - 1) / blkq;
+  a.nkb = (Nkv + blkk - 1) / blkk;
+  const bool need_b = a.smooth_k || a.v_fp8;
+  a.n_stat = need_b ? a.nch * Hkv * B : 0;
+  a.n_qblk = a.nqb * Hq * B;
+  a.n_kblk_a = need_b ? 0 : a.nkb * Hkv * B;
+  if (a.n_stat + a.n_qblk + a.n_kblk_a > 0x7FFFFFFF || a.nkb * Hkv * B > 0x7FFFFFFF)
+    return fail("sage_prepass: invalid argument: grid too large");
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case SAGE_DTYPE_F32:
+      return D == 64 ? launch_prepass<float, 64>(a, st) : launch_prepass<float, 128>(a, st);
+    case SAGE_DTYPE_F16:
+      return D == 64 ? launch_prepass<_Float16, 64>(a, st) : launch_prepass<_Float16, 128>(a, st);
+    default:
+      return D == 64 ? launch_prepass<__bf16, 64>(a, st) : launch_prepass<__bf16, 128>(a, st);
+  }
+}

@@ -1,0 +1,251 @@
+"""HIP variant of the sage_attn kernel pack (MI355X / gfx950).
+
+``run`` has the call signature of ``run_sage_attn`` (triton_impl.py:162) and
+is registered as ``variants: {"hip": "hip_impl.py:run"}`` in meta.json, so the
+harness's ``test`` and ``run`` commands drive it unchanged.  It allocates every
+buffer with torch on the inputs' device and calls the C ABI of
+``libsage_attn.so`` (include/sage_attn.h) through ctypes, on torch's current
+stream:
+
+    sage_prepass   per_block_int8 (triton_impl.py:35-82) + K smoothing (+ FP8 V)
+    sage_attn_fwd  _attn_fwd launch (triton_impl.py:186-199)
+
+There is no CPU or PyTorch fallback: without a ROCm device or without the
+library the call raises.  The module is loaded by file path (no parent
+package), so it finds the library from its own location:
+``$TRIBENCH_SAGE_HIP_LIB``, ``./libsage_attn.so`` next to this file, or
+``tribench_amd/lib/libsage_attn.so`` of this repository.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ABI_VERSION = 1
+LOG2E_REF = 1.44269504  # triton_impl.py:69
+WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
+
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_FP8E4M3 = 0, 1, 2, 3
+V_NONE, V_FP8 = 0, 1
+PV_MODES = {"fp16": 0, "bf16": 1, "fp8": 2}
+_TORCH_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
+
+_LIB = None
+
+
+def library_path() -> Path:
+    """Where the C-ABI library is looked up (first existing candidate)."""
+    here = Path(__file__).resolve().parent
+    cands = []
+    env = os.environ.get("TRIBENCH_SAGE_HIP_LIB")
+    if env:
+        cands.append(Path(env))
+    cands.append(here / "libsage_attn.so")
+    cands.append(here.parents[1] / "lib" / "libsage_attn.so")
+    for c in cands:
+        if c.is_file():
+            return c
+    raise RuntimeError(
+        "sage_attn hip: libsage_attn.so not found (looked in: "
+        + ", ".join(str(c) for c in cands) + "); build it with `python -m tribench_amd.build`"
+    )
+
+
+def _load():
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    lib = ctypes.CDLL(str(library_path()))
+    i64, i32, f32, vp, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+    p64 = ctypes.POINTER(ctypes.c_int64)
+    lib.sage_abi_version.restype = i32
+    lib.sage_abi_version.argtypes = []
+    lib.sage_last_error.restype = ctypes.c_char_p
+    lib.sage_last_error.argtypes = []
+    lib.sage_prepass_workspace_bytes.restype = sz
+    lib.sage_prepass_workspace_bytes.argtypes = [i64, i64, i64, i64, i32, i32]
+    lib.sage_prepass.restype = i32
+    lib.sage_prepass.argtypes = [
+        vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, p64, p64, p64, f32, i32, i32, i32, i32, i32,
+        vp, p64, vp, vp, p64, vp, vp, vp, p64, vp, vp, sz, vp,
+    ]
+    lib.sage_attn_fwd.restype = i32
+    lib.sage_attn_fwd.argtypes = [
+        vp, p64, vp, vp, p64, vp, vp, i32, p64, vp, vp, i32, p64, i64, i64, i64, i64, i64, i64, i32,
+        i32, i32, i32, i32, vp,
+    ]
+    ver = lib.sage_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"sage_attn hip: library ABI {ver}, expected {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = _load().sage_last_error().decode(errors="replace")
+        raise RuntimeError(f"sage_attn hip: {what} failed: {msg}")
+
+
+def _strides(t: torch.Tensor, layout: str):
+    """(batch, head, seq) element strides of a 4-D tensor in the given layout."""
+    s = t.stride()
+    if layout == "HND":
+        vals = (s[0], s[1], s[2])
+    elif layout == "NHD":
+        vals = (s[0], s[2], s[1])
+    else:
+        raise ValueError(f"sage_attn hip: invalid argument: tensor_layout {layout!r}")
+    return (ctypes.c_int64 * 3)(*vals)
+
+
+def _dims(t: torch.Tensor, layout: str):
+    if layout == "HND":
+        b, h, n, d = t.shape
+    else:
+        b, n, h, d = t.shape
+    return b, h, n, d
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _check_inputs(q, k, v, layout):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not isinstance(t, torch.Tensor):
+            raise TypeError(f"sage_attn hip: invalid argument: {name} is not a tensor")
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"sage_attn hip: {name} is on {t.device}; this variant runs only on a ROCm GPU device")
+        if t.dim() != 4 or t.stride(3) != 1:
+            raise ValueError(f"sage_attn hip: invalid argument: {name} must be 4-D with a unit head-dim stride")
+        if t.dtype not in _TORCH_CODES:
+            raise ValueError(f"sage_attn hip: invalid argument: {name} dtype {t.dtype}")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("sage_attn hip: invalid argument: q, k, v dtypes differ")
+    if not (q.device == k.device == v.device):
+        raise ValueError("sage_attn hip: invalid argument: q, k, v devices differ")
+    B, Hq, Nq, D = _dims(q, layout)
+    Bk, Hkv, Nkv, Dk = _dims(k, layout)
+    if _dims(v, layout) != (Bk, Hkv, Nkv, Dk) or Bk != B or Dk != D:
+        raise ValueError(f"sage_attn hip: invalid argument: shape mismatch q{tuple(q.shape)} "
+                         f"k{tuple(k.shape)} v{tuple(v.shape)}")
+    if Hq % Hkv:
+        raise ValueError(f"sage_attn hip: invalid argument: {Hq} query heads not a multiple of {Hkv} kv heads")
+    return B, Hq, Hkv, Nq, Nkv, D
+
+
+def _empty_like_layout(t: torch.Tensor, dtype) -> torch.Tensor:
+    return torch.empty_like(t, dtype=dtype, memory_format=torch.preserve_format)
+
+
+def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smooth_k=True,
+            v_fp8=False, tensor_layout="HND"):
+    """Run the HIP pre-pass; returns a dict of device tensors.
+
+    q8/k8 (int8, same layout as q/k), q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)],
+    k_scale [B,Hkv,ceil(Nkv/blkk)], km [B,Hkv,D] (smooth_k), and v8 (e4m3 codes
+    as uint8) + v_scale [B,Hkv,D] (v_fp8).
+    """
+    lib = _load()
+    B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v if v is not None else k, tensor_layout)
+    q_sub = blkq if q_sub is None else q_sub
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    q_mul = float(np.float32(sm_scale * LOG2E_REF))
+    dev = q.device
+    q8 = _empty_like_layout(q, torch.int8)
+    k8 = _empty_like_layout(k, torch.int8)
+    nqs = -(-Nq // blkq) * (blkq // q_sub)
+    q_scale = torch.empty((B, Hq, nqs), dtype=torch.float32, device=dev)
+    k_scale = torch.empty((B, Hkv, -(-Nkv // blkk)), dtype=torch.float32, device=dev)
+    km = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev) if smooth_k else None
+    v8 = v_scale = None
+    if v_fp8:
+        v8 = _empty_like_layout(v, torch.uint8)
+        v_scale = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev)
+    ws_bytes = lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), V_FP8 if v_fp8 else V_NONE)
+    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    rc = lib.sage_prepass(
+        _ptr(q), _ptr(k), _ptr(v) if v_fp8 else None, _TORCH_CODES[q.dtype], B, Hq, Hkv, Nq, Nkv, D,
+        _strides(q, tensor_layout), _strides(k, tensor_layout),
+        _strides(v, tensor_layout) if v_fp8 else None,
+        q_mul, blkq, blkk, q_sub, int(smooth_k), V_FP8 if v_fp8 else V_NONE,
+        _ptr(q8), _strides(q8, tensor_layout), _ptr(q_scale), _ptr(k8), _strides(k8, tensor_layout),
+        _ptr(k_scale), _ptr(km), _ptr(v8), _strides(v8, tensor_layout) if v_fp8 else None, _ptr(v_scale),
+        _ptr(ws), ctypes.c_size_t(ws_bytes), _stream(dev),
+    )
+    _check(rc, "sage_prepass")
+    out = {"q8": q8, "q_scale": q_scale, "k8": k8, "k_scale": k_scale, "workspace": ws}
+    if smooth_k:
+        out["km"] = km
+    if v_fp8:
+        out["v8"] = v8
+        out["v_scale"] = v_scale
+    return out
+
+
+def per_block_int8(q, k, km=None, BLKQ=128, BLKK=64, sm_scale=None, tensor_layout="HND"):
+    """HIP counterpart of per_block_int8 (triton_impl.py:35-82).
+
+    Returns (q_int8, q_scale, k_int8, k_scale).  A caller-supplied ``km`` is
+    subtracted from k in k's dtype first, as the reference does (:39-40).
+    """
+    if km is not None:
+        k = k - km
+    r = prepass(q, k, k, sm_scale, blkq=BLKQ, blkk=BLKK, smooth_k=False, tensor_layout=tensor_layout)
+    return r["q8"], r["q_scale"], r["k8"], r["k_scale"]
+
+
+def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
+        tensor_layout="HND", return_intermediates=False, **kw):
+    """SageAttention forward on MI355X: INT8 QK^T, online softmax, P.V.
+
+    Same call as run_sage_attn(q, k, v, causal=False, sm_scale=None)
+    (triton_impl.py:162): q [B,Hq,N,D], k/v [B,Hkv,N,D] (HND), fp16/bf16/fp32,
+    returns o with q's shape and dtype.  Unlike the reference, ``causal`` is
+    honoured.  Options (case keys of meta.json arrive here):
+
+    pv_dtype   "fp16" (the reference's P.V type), "bf16", or "fp8" (FP8 e4m3 P
+               and per-channel FP8 V)
+    q_gran     "block": one Q scale per 128 rows (reference); "wave": one per
+               32 rows (the attention kernel's per-wavefront tile)
+    smooth_k   subtract the per-channel K mean before quantizing (default on)
+    """
+    lib = _load()
+    if pv_dtype not in PV_MODES:
+        raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
+    if q_gran not in ("block", "wave"):
+        raise ValueError(f"sage_attn hip: invalid argument: q_gran {q_gran!r}")
+    B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
+    blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
+    q_sub = WAVE_ROWS if q_gran == "wave" else blkq
+    v_fp8 = pv_dtype == "fp8"
+    pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k, v_fp8=v_fp8,
+                  tensor_layout=tensor_layout)
+    o = _empty_like_layout(q, q.dtype)
+    if v_fp8:
+        v_in, v_code, v_str = pre["v8"], DTYPE_FP8E4M3, _strides(pre["v8"], tensor_layout)
+    else:
+        v_in, v_code, v_str = v, _TORCH_CODES[v.dtype], _strides(v, tensor_layout)
+    rc = lib.sage_attn_fwd(
+        _ptr(pre["q8"]), _strides(pre["q8"], tensor_layout), _ptr(pre["q_scale"]),
+        _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
+        _ptr(v_in), v_code, v_str, _ptr(pre.get("v_scale")),
+        _ptr(o), _TORCH_CODES[o.dtype], _strides(o, tensor_layout),
+        B, Hq, Hkv, Nq, Nkv, D, int(bool(causal)), blkq, blkk, q_sub, PV_MODES[pv_dtype], _stream(q.device),
+    )
+    _check(rc, "sage_attn_fwd")
+    if return_intermediates:
+        pre.pop("workspace", None)
+        return o, pre
+    return o
