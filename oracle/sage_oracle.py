@@ -151,7 +151,8 @@ def e4m3_encode(x):
     af = a.view(np.float32)
     code = np.zeros(x.shape, dtype=np.uint32)
     sub = af < np.float32(2.0 ** -6)
-    code = np.where(sub, np.rint(af * np.float32(512.0)).astype(np.uint32), code)
+    sub_code = np.rint(np.minimum(af, np.float32(1.0)) * np.float32(512.0)).astype(np.uint32)
+    code = np.where(sub, sub_code, code)
     e = (a >> np.uint32(23)).astype(np.int64) - 127 + 7
     m = a & np.uint32(0x7FFFFF)
     m3 = m >> np.uint32(20)

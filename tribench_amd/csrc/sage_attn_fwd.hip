@@ -27,6 +27,8 @@
 //  * Work-group ids are remapped so that all q-blocks of one (batch, kv head)
 //    run on the same XCD (shared L2) — the hardware deals work-groups to the 8
 //    XCDs round-robin.
+#include <stdlib.h>
+
 #include "sage_device.h"
 
 namespace sage {
@@ -39,11 +41,12 @@ struct AttnArgs {
   const void* v;
   const float* v_scale;
   void* o;
-  int64_t sq[3], sk[3], sv[3], so[3];
+  int64_t sq[2], sk[2], sv[2], so[2];  // batch and head strides (elements)
+  int sqn, skn, svn, son;              // row strides (elements); row offsets fit 32 bits
   int B, Hq, Hkv, Nq, Nkv;
   int causal;
-  int q_sub, blkk;
-  int nqs, nks;  // q / k scales per head
+  int q_sub, blkk_shift;  // k scale of key block j: k_scale[j >> blkk_shift]
+  int nqs, nks;           // q / k scales per head
 };
 
 template <typename P>
@@ -51,6 +54,7 @@ struct PvOps;
 template <>
 struct PvOps<_Float16> {
   typedef v8h V8;
+  __device__ static __forceinline__ v4i ones() { return (v4i){0x3C003C00, 0x3C003C00, 0x3C003C00, 0x3C003C00}; }
   __device__ static __forceinline__ uint32_t pack2(float a, float b) {
     h2 r = __builtin_convertvector((f2){a, b}, h2);
     return __builtin_bit_cast(uint32_t, r);
@@ -63,6 +67,7 @@ struct PvOps<_Float16> {
 template <>
 struct PvOps<__bf16> {
   typedef v8bf V8;
+  __device__ static __forceinline__ v4i ones() { return (v4i){0x3F803F80, 0x3F803F80, 0x3F803F80, 0x3F803F80}; }
   __device__ static __forceinline__ uint32_t pack2(float a, float b) {
     bf2 r = __builtin_convertvector((f2){a, b}, bf2);
     return __builtin_bit_cast(uint32_t, r);
@@ -90,42 +95,67 @@ __device__ __forceinline__ void store4<__bf16>(__bf16* p, float a, float b, floa
   *reinterpret_cast<v2i*>(p) = w;
 }
 
-// byte offset of 16-byte chunk L (= row * chunks_per_row + col) of a K8 tile
-__device__ __forceinline__ int k_lds_off(int L) {
-  const int line = L >> 3, pos = L & 7;
-  return (line << 7) + ((pos ^ (line & 7)) << 4);
-}
-// byte offset of 8-byte chunk c (4 keys) of row d of the V^T tile (64 keys)
-__device__ __forceinline__ int v_lds_off(int d, int c) {
-  return (d << 7) + ((c ^ ((d ^ (d >> 3)) & 15)) << 3);
-}
-
+// ---------------------------------------------------------------------------
+// LDS layouts (rows padded instead of swizzled, so every operand read is one
+// per-lane base plus a compile-time offset and both reads and staging writes
+// are bank-conflict free).  A tile holds the BNI = 64*SUB keys of one
+// iteration:
+//  K8 tile  [BNI keys][D] int8, row pitch D + 16 bytes
+//  V^T tile [D][BNI keys] 16-bit, row pitch 2*BNI + 8 bytes
+// ---------------------------------------------------------------------------
 __device__ __forceinline__ int remap_xcd(int w, int n) {
   const int per = n >> 3, rem = n & 7;
   const int xcd = w & 7, loc = w >> 3;
   return xcd * per + min(xcd, rem) + loc;
 }
 
-template <int D, int NW, int QW, typename TV, typename PV, typename TO>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
+// max over the lanes {l, l^16, l^32, l^48} (the four lane groups holding one
+// q column of the score tile) with the gfx950 permlane swaps
+__device__ __forceinline__ int max_over_groups(int v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  v = max((int)a[0], (int)a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return max((int)b[0], (int)b[1]);
+}
+
+// The int32 MFMA accumulator starts at the bit pattern of 2^23 + 2^22, so
+// it reads as the float 12582912 + S, exact for |S| < 2^22 (|S| <= 127^2*D).
+constexpr int kMagicI = 0x4B400000;
+constexpr float kMagicF = 12582912.0f;
+// A row's running max is only moved when a block's max exceeds it by more
+// than kTau (log2 units); P values are then bounded by 2^kTau.
+constexpr float kTau = 8.0f;
+
+// NW waves of QW query rows each; SUB 64-key sub-blocks per iteration (one
+// barrier and one prefetch per iteration).  One work-group per CU: NW/4 waves
+// per SIMD, so the compiler may use the whole register file.
+template <int D, int NW, int QW, int SUB, typename TV, typename PV, typename TO>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void attn_fwd_kernel(
+    AttnArgs a) {
   constexpr int NT = NW * 64;
-  constexpr int BM = NW * QW;  // q rows per work-group
-  constexpr int BN = 64;       // keys per block
-  constexpr int QT = QW / 16;  // q tiles per wave
-  constexpr int DH = D / 64;   // 64-wide slices of the QK contraction
-  constexpr int DT = D / 16;   // 16-row d tiles of O^T
-  constexpr int KT = BN / 16;  // 16-key tiles per block
-  constexpr int CPR = D / 16;  // 16-byte chunks per K8 row
-  constexpr int K_BYTES = BN * D;
-  constexpr int V_BYTES = D * BN * 2;
-  constexpr int BUF = K_BYTES + V_BYTES;
-  constexpr int KCH = BN * CPR;             // K8 chunks per tile
+  constexpr int BM = NW * QW;   // q rows per work-group
+  constexpr int BN = 64;        // keys per softmax block (one k scale)
+  constexpr int BNI = BN * SUB; // keys per iteration
+  constexpr int QT = QW / 16;   // q tiles per wave
+  constexpr int DH = D / 64;    // 64-wide slices of the QK contraction
+  constexpr int DT = D / 16;    // 16-row d tiles of O^T
+  constexpr int KT = BN / 16;   // 16-key tiles per block
+  constexpr int CPR = D / 16;   // 16-byte chunks per K8 row
+  constexpr int KP = D + 16;    // K8 row pitch in LDS
+  constexpr int VPI = 2 * BNI + 8;  // V^T row pitch in LDS
+  constexpr int KB = BNI * KP;      // bytes of a K8 tile
+  constexpr int VB = D * VPI;       // bytes of a V^T tile
+  constexpr int KCH = BNI * CPR;            // 16-byte K8 chunks per tile
+  constexpr int VMT = (BNI / 2) * (D / 8);  // 2-key x 8-d micro-tiles per V tile
+  static_assert(KCH % 64 == 0 && VMT % 64 == 0, "staging work must be whole waves");
   constexpr int KCH_T = (KCH + NT - 1) / NT;
-  constexpr int VMT = (BN / 4) * (D / 8);   // 4-key x 8-d micro-tiles per V tile
   constexpr int VMT_T = (VMT + NT - 1) / NT;
   using Ops = PvOps<PV>;
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * BUF];
+  __shared__ __attribute__((aligned(16))) char smem[2 * KB + 2 * VB];
+  __shared__ float ksc_s[2][SUB];  // k scales of the tile in each buffer
+  char* const kbuf0 = smem;
+  char* const vbuf0 = smem + 2 * KB;
 
   const int nqb = (a.Nq + BM - 1) / BM;
   const int wg = remap_xcd((int)blockIdx.x, (int)gridDim.x);
@@ -136,7 +166,8 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   const int hk = h / (a.Hq / a.Hkv);
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
   const int q0 = qb * BM;
   const int qa = q0 + wave * QW;  // first q row of this wave
@@ -146,179 +177,275 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   const TV* vbase = static_cast<const TV*>(a.v) + b * a.sv[0] + hk * a.sv[1];
   const float* ksc_base = a.k_scale + ((int64_t)b * a.Hkv + hk) * a.nks;
 
-  // ---- Q (B operand of S^T = K Q^T): q = qa + 16s + n, d = 64hh + 16g .. +16
+  // ---- Q (B operand of S^T = K Q^T): q = qa + 16s + n, d = 64hh + 16g .. +16.
+  // Rows past Nq read the last row; their results are never stored.
   v4i qreg[QT][DH];
   float qsc[QT];
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    const int row = qa + 16 * s + n;
+    const int row = min(qa + 16 * s + n, a.Nq - 1);
 #pragma unroll
-    for (int hh = 0; hh < DH; ++hh) {
-      qreg[s][hh] = (v4i){0, 0, 0, 0};
-      if (row < a.Nq) qreg[s][hh] = *reinterpret_cast<const v4i*>(qbase + row * a.sq[2] + 64 * hh + 16 * g);
-    }
+    for (int hh = 0; hh < DH; ++hh)
+      qreg[s][hh] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 64 * hh + 16 * g));
     const int si = min((qa + 16 * s) / a.q_sub, a.nqs - 1);
     qsc[s] = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + si];
   }
 
-  // ---- key range
+  // ---- key range (in 64-key blocks) of the work-group and of this wave
   const int nkb_all = (a.Nkv + BN - 1) / BN;
   int nkb = nkb_all;
   if (a.causal) nkb = min(nkb_all, (min(q0 + BM, a.Nq) - 1) / BN + 1);
+  const int nit = (nkb + SUB - 1) / SUB;      // iterations
   const int q_last = min(qa + QW, a.Nq) - 1;  // last valid row of this wave (< qa if none)
+  int jmax = nkb - 1;                          // last 64-key block this wave needs
+  if (q_last < qa) jmax = -1;
+  else if (a.causal) jmax = min(jmax, q_last / BN);
 
-  // ---- staging registers
+  // ---- per-lane LDS read bases; tiles and halves are immediate offsets
+  const int kread = n * KP + 16 * g;   // + (64*sb + 16*t)*KP + 64*hh
+  const int vread = n * VPI + 8 * g;   // + dt*16*VPI + 2*(64*sb + 32*u + 16*hf)
+
+  // ---- staging.  K8: chunk L = tid + i*NT -> row L/CPR, column L%CPR.
+  // V: micro-tile m = tid + i*NT -> keys 2*(m%(BNI/2)) + {0,1}, d = 8*(m/(BNI/2)) .. +8.
+  // Keys past Nkv read the last key: their P is 0 and the data is finite.
   v4i kst[KCH_T];
-  Raw8<TV> vst[VMT_T][4];
-
-  auto stage_load = [&](int j) {
-    const int k0 = j * BN;
+  Raw8<TV> vst[VMT_T][2];
+  float kscst = 0.0f;  // lanes 0..SUB-1 of wave 0: the tile's k scales
+  auto load_tile = [&](int it) {
+    const int k0 = it * BNI;
+    if (wave == 0 && lane < SUB) kscst = ksc_base[min((it * SUB + lane) >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int i = 0; i < KCH_T; ++i) {
-      const int L = tid + i * NT;
-      kst[i] = (v4i){0, 0, 0, 0};
-      if (L < KCH) {
-        const int row = L / CPR, c = L % CPR;
-        if (k0 + row < a.Nkv) kst[i] = *reinterpret_cast<const v4i*>(kbase + (k0 + row) * a.sk[2] + 16 * c);
+      if (wave * 64 + i * NT < KCH) {
+        const int L = tid + i * NT;
+        const int row = min(k0 + L / CPR, a.Nkv - 1);
+        kst[i] = *reinterpret_cast<const v4i*>(kbase + (uint32_t)(row * a.skn + 16 * (L % CPR)));
       }
     }
 #pragma unroll
     for (int i = 0; i < VMT_T; ++i) {
-      const int m = tid + i * NT;
-      if (m < VMT) {
-        const int dg = m % (D / 8), kq = m / (D / 8);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = k0 + 4 * kq + r;
-          vst[i][r] = key < a.Nkv ? load8<TV>(vbase + key * a.sv[2] + 8 * dg) : zero8<TV>();
-        }
+      if (wave * 64 + i * NT < VMT) {
+        const int m = tid + i * NT;
+        const int key = k0 + 2 * (m % (BNI / 2));
+        const int col = 8 * (m / (BNI / 2));
+        vst[i][0] = load8<TV>(vbase + (uint32_t)(min(key, a.Nkv - 1) * a.svn + col));
+        vst[i][1] = load8<TV>(vbase + (uint32_t)(min(key + 1, a.Nkv - 1) * a.svn + col));
       }
     }
   };
-  auto stage_store = [&](int buf) {
-    char* ks = smem + buf * BUF;
-    char* vs = ks + K_BYTES;
+  auto store_tile = [&](int buf) {
+    char* ks = kbuf0 + buf * KB;
+    char* vs = vbuf0 + buf * VB;
+    if (wave == 0 && lane < SUB) ksc_s[buf][lane] = kscst;
 #pragma unroll
     for (int i = 0; i < KCH_T; ++i) {
-      const int L = tid + i * NT;
-      if (L < KCH) *reinterpret_cast<v4i*>(ks + k_lds_off(L)) = kst[i];
+      if (wave * 64 + i * NT < KCH) {
+        const int L = tid + i * NT;
+        *reinterpret_cast<v4i*>(ks + (L / CPR) * KP + 16 * (L % CPR)) = kst[i];
+      }
     }
 #pragma unroll
     for (int i = 0; i < VMT_T; ++i) {
-      const int m = tid + i * NT;
-      if (m < VMT) {
-        const int dg = m % (D / 8), kq = m / (D / 8);
+      if (wave * 64 + i * NT < VMT) {
+        const int m = tid + i * NT;
+        char* dst = vs + 8 * (m / (BNI / 2)) * VPI + 4 * (m % (BNI / 2));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          v2i w;
-          w.x = (int)Ops::pack2(elem<TV>(vst[i][0], e), elem<TV>(vst[i][1], e));
-          w.y = (int)Ops::pack2(elem<TV>(vst[i][2], e), elem<TV>(vst[i][3], e));
-          *reinterpret_cast<v2i*>(vs + v_lds_off(8 * dg + e, kq)) = w;
-        }
+        for (int e = 0; e < 8; ++e)
+          *reinterpret_cast<uint32_t*>(dst + e * VPI) = Ops::pack2(elem<TV>(vst[i][0], e), elem<TV>(vst[i][1], e));
       }
     }
   };
 
   // ---- accumulators
   v4f oacc[DT][QT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int s = 0; s < QT; ++s) oacc[dt][s] = (v4f){0.f, 0.f, 0.f, 0.f};
-  float m_i[QT], l_i[QT];
+  v4f lacc[QT];  // row sums of P via MFMA with an all-ones A operand
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    m_i[s] = -INFINITY;
-    l_i[s] = 0.0f;
+    lacc[s] = (v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) oacc[dt][s] = (v4f){0.f, 0.f, 0.f, 0.f};
   }
+  float m_use[QT];
+#pragma unroll
+  for (int s = 0; s < QT; ++s) m_use[s] = -INFINITY;
+  const v4i ones = Ops::ones();
 
-  stage_load(0);
-  stage_store(0);
-  __syncthreads();
-
-  for (int j = 0; j < nkb; ++j) {
-    const bool has_next = j + 1 < nkb;
-    if (has_next) stage_load(j + 1);
-    const int k0 = j * BN;
-    const bool active = q_last >= qa && (!a.causal || k0 <= q_last);
-    if (active) {
-      const char* ks = smem + (j & 1) * BUF;
-      const char* vs = ks + K_BYTES;
-      // S^T = K Q^T
-      v4i sacc[KT][QT];
+  // ---- building blocks.  Operand reads are separate from the MFMAs that
+  // use them so a phase can issue its reads first; the generic path fences
+  // reads from MFMAs with a scheduling barrier, the hot path interleaves them
+  // explicitly (see below).
+  // K8 operand (t, hh) of sub-block sb: rows 16t + n, bytes 64hh + 16g .. +16
+  auto read_k = [&](int buf, int sb, v4i (&ka)[KT][DH]) {
+    const char* ks = kbuf0 + buf * KB + kread + sb * 64 * KP;
 #pragma unroll
-      for (int t = 0; t < KT; ++t) {
+    for (int t = 0; t < KT; ++t)
 #pragma unroll
-        for (int s = 0; s < QT; ++s) sacc[t][s] = (v4i){0, 0, 0, 0};
+      for (int hh = 0; hh < DH; ++hh) ka[t][hh] = *reinterpret_cast<const v4i*>(ks + t * 16 * KP + 64 * hh);
+  };
+  auto mma_qk = [&](const v4i (&ka)[KT][DH], v4i (&sacc)[KT][QT]) {
 #pragma unroll
-        for (int hh = 0; hh < DH; ++hh) {
-          const v4i ka = *reinterpret_cast<const v4i*>(ks + k_lds_off((16 * t + n) * CPR + 4 * hh + g));
+    for (int t = 0; t < KT; ++t) {
 #pragma unroll
-          for (int s = 0; s < QT; ++s)
-            sacc[t][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, qreg[s][hh], sacc[t][s], 0, 0, 0);
+      for (int s = 0; s < QT; ++s) sacc[t][s] = (v4i){kMagicI, kMagicI, kMagicI, kMagicI};
+#pragma unroll
+      for (int hh = 0; hh < DH; ++hh)
+#pragma unroll
+        for (int s = 0; s < QT; ++s)
+          sacc[t][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[t][hh], qreg[s][hh], sacc[t][s], 0, 0, 0);
+    }
+  };
+  // V^T operand (dt) of half u of sub-block sb: rows 16dt + n, keys
+  // 32u + 4g..+3 and 32u + 16 + 4g..+3 of the sub-block
+  auto read_v = [&](int buf, int sb, int u, v4i (&va)[DT]) {
+    const char* vs = vbuf0 + buf * VB + vread + sb * 128 + 64 * u;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const v2i lo = *reinterpret_cast<const v2i*>(vs + dt * 16 * VPI);
+      const v2i hi = *reinterpret_cast<const v2i*>(vs + dt * 16 * VPI + 32);
+      va[dt] = (v4i){lo.x, lo.y, hi.x, hi.y};
+    }
+  };
+  auto mma_pv = [&](const v4i (&va)[DT], int u, const v4i (&pk)[QT][2]) {
+#pragma unroll
+    for (int s = 0; s < QT; ++s) lacc[s] = Ops::mfma(ones, pk[s][u], lacc[s]);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s = 0; s < QT; ++s) oacc[dt][s] = Ops::mfma(va[dt], pk[s][u], oacc[dt][s]);
+  };
+  auto qk = [&](int buf, int sb, v4i (&sacc)[KT][QT]) {
+    v4i ka[KT][DH];
+    read_k(buf, sb, ka);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_qk(ka, sacc);
+  };
+  auto pv = [&](int buf, int sb, const v4i (&pk)[QT][2]) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      v4i va[DT];
+      read_v(buf, sb, u, va);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_pv(va, u, pk);
+    }
+  };
+  auto key_ok = [&](int key, int qrow) { return key < a.Nkv && (!a.causal || key <= qrow); };
+  // block max of each q column of 64-key block kb (log2 units; -inf if all masked)
+  auto rowmax = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], float (&mblk)[QT], bool masked) {
+    const int k0 = kb * BN;
+#pragma unroll
+    for (int s = 0; s < QT; ++s) {
+      const int qrow = qa + 16 * s + n;
+      int mx = INT_MIN;
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int v = sacc[t][s][r];
+          if (masked) v = key_ok(k0 + 16 * t + 4 * g + r, qrow) ? v : INT_MIN;
+          mx = max(mx, v);
         }
-      }
-      const float ksc = ksc_base[k0 / a.blkk];
-      const bool masked = (k0 + BN > a.Nkv) || (a.causal && k0 + BN - 1 > qa);
-      // online softmax (base 2) and P in B-operand layout
-      v4i pk[QT][2];
+      mx = max_over_groups(mx);
+      mblk[s] = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * (qsc[s] * ksc);
+    }
+  };
+  // lazy max update: returns whether O and the row sums must be rescaled by
+  // alpha[] (wave-uniform; applied by the caller at the right point)
+  auto decide = [&](const float (&mblk)[QT], float (&alpha)[QT]) -> bool {
+    bool need = false;
+#pragma unroll
+    for (int s = 0; s < QT; ++s) need |= mblk[s] > m_use[s] + kTau;
+    const bool rescale = __builtin_amdgcn_ballot_w64(need) != 0;
+#pragma unroll
+    for (int s = 0; s < QT; ++s) alpha[s] = 1.0f;
+    if (rescale) {
 #pragma unroll
       for (int s = 0; s < QT; ++s) {
-        const float c = qsc[s] * ksc;
-        const int qrow = qa + 16 * s + n;
-        int mx = INT_MIN;
-#pragma unroll
-        for (int t = 0; t < KT; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = k0 + 16 * t + 4 * g + r;
-            const bool ok = !masked || (key < a.Nkv && (!a.causal || key <= qrow));
-            if (ok) mx = max(mx, sacc[t][s][r]);
-          }
-        mx = max(mx, __shfl_xor(mx, 16));
-        mx = max(mx, __shfl_xor(mx, 32));
-        const float mblk = mx == INT_MIN ? -INFINITY : (float)mx * c;
-        const float mnew = fmaxf(m_i[s], mblk);
-        const float alpha = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_i[s] - mnew);
-        const float msub = mnew == -INFINITY ? 0.0f : mnew;
-        m_i[s] = mnew;
-        l_i[s] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha;
-        float p[KT][4];
-#pragma unroll
-        for (int t = 0; t < KT; ++t)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int key = k0 + 16 * t + 4 * g + r;
-            const bool ok = !masked || (key < a.Nkv && (!a.causal || key <= qrow));
-            const float x = __builtin_fmaf((float)sacc[t][s][r], c, -msub);
-            p[t][r] = ok ? __builtin_amdgcn_exp2f(x) : 0.0f;
-            l_i[s] += p[t][r];
-          }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          pk[s][u].x = (int)Ops::pack2(p[2 * u][0], p[2 * u][1]);
-          pk[s][u].y = (int)Ops::pack2(p[2 * u][2], p[2 * u][3]);
-          pk[s][u].z = (int)Ops::pack2(p[2 * u + 1][0], p[2 * u + 1][1]);
-          pk[s][u].w = (int)Ops::pack2(p[2 * u + 1][2], p[2 * u + 1][3]);
-        }
-      }
-      // O^T += V^T P^T
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const int d = 16 * dt + n;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const v2i lo = *reinterpret_cast<const v2i*>(vs + v_lds_off(d, 8 * u + g));
-          const v2i hi = *reinterpret_cast<const v2i*>(vs + v_lds_off(d, 8 * u + 4 + g));
-          const v4i va = {lo.x, lo.y, hi.x, hi.y};
-#pragma unroll
-          for (int s = 0; s < QT; ++s) oacc[dt][s] = Ops::mfma(va, pk[s][u], oacc[dt][s]);
-        }
+        const float mn = fmaxf(m_use[s], mblk[s]);
+        alpha[s] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[s] - mn);
+        m_use[s] = mn;
       }
     }
-    if (has_next) stage_store((j + 1) & 1);
+    return rescale;
+  };
+  // P = exp2(S*c - m) of q tile s in B-operand layout (16-bit pairs)
+  auto exps_s = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2], int s, bool masked) {
+    const int k0 = kb * BN;
+    {
+      const float c = qsc[s] * ksc;
+      const float m = m_use[s] == -INFINITY ? 0.0f : m_use[s];
+      const float bias = __builtin_fmaf(kMagicF, c, m);  // x = (2^23+2^22+S)*c - bias = S*c - m
+      const int qrow = qa + 16 * s + n;
+      float p[KT][4];
+#pragma unroll
+      for (int t = 0; t < KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float x = __builtin_fmaf(__int_as_float(sacc[t][s][r]), c, -bias);
+          float e = __builtin_amdgcn_exp2f(x);
+          if (masked) e = key_ok(k0 + 16 * t + 4 * g + r, qrow) ? e : 0.0f;
+          p[t][r] = e;
+        }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        pk[s][u].x = (int)Ops::pack2(p[2 * u][0], p[2 * u][1]);
+        pk[s][u].y = (int)Ops::pack2(p[2 * u][2], p[2 * u][3]);
+        pk[s][u].z = (int)Ops::pack2(p[2 * u + 1][0], p[2 * u + 1][1]);
+        pk[s][u].w = (int)Ops::pack2(p[2 * u + 1][2], p[2 * u + 1][3]);
+      }
+    }
+  };
+  auto exps = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2], bool masked) {
+#pragma unroll
+    for (int s = 0; s < QT; ++s) exps_s(kb, ksc, sacc, pk, s, masked);
+  };
+  auto apply_rescale = [&](const float (&alpha)[QT]) {
+#pragma unroll
+    for (int s = 0; s < QT; ++s) {
+      lacc[s] *= alpha[s];
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha[s];
+    }
+  };
+  auto is_masked = [&](int kb) {
+    const int k0 = kb * BN;
+    return (k0 + BN > a.Nkv) || (a.causal && k0 + BN - 1 > qa);
+  };
+  // generic order for one 64-key block (masked blocks, partially active tiles)
+  auto block_generic = [&](int buf, int sb, int kb, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2]) {
+    const float ksc = ksc_s[buf][sb];
+    const bool masked = is_masked(kb);
+    float mblk[QT], alpha[QT];
+    if (masked) rowmax(kb, ksc, sacc, mblk, true);
+    else rowmax(kb, ksc, sacc, mblk, false);
+    if (decide(mblk, alpha)) apply_rescale(alpha);
+    if (masked) exps(kb, ksc, sacc, pk, true);
+    else exps(kb, ksc, sacc, pk, false);
+    pv(buf, sb, pk);
+  };
+
+  // ---- main loop: iteration it stages tile it+1 (global loads in flight
+  // during the compute) and computes the SUB 64-key blocks of tile it.  The
+  // QK of every sub-block is issued before the first softmax.
+  load_tile(0);
+  store_tile(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int it = 0; it < nit; ++it) {
+    const bool more = it + 1 < nit;
+    if (more) load_tile(it + 1);
+    const int buf = it & 1;
+    const int kb0 = it * SUB;
+    if (kb0 <= jmax) {
+      v4i S[SUB][KT][QT];
+      v4i P[QT][2];
+#pragma unroll
+      for (int sb = 0; sb < SUB; ++sb)
+        if (kb0 + sb <= jmax) qk(buf, sb, S[sb]);
+#pragma unroll
+      for (int sb = 0; sb < SUB; ++sb)
+        if (kb0 + sb <= jmax) block_generic(buf, sb, kb0 + sb, S[sb], P);
+    }
+    if (more) store_tile((it + 1) & 1);
     __syncthreads();
   }
 
@@ -326,29 +453,43 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_kernel(AttnArgs a) {
   TO* obase = static_cast<TO*>(a.o) + b * a.so[0] + h * a.so[1];
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    float l = l_i[s];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const float inv = 1.0f / l;
+    const float inv = 1.0f / lacc[s][0];
     const int row = qa + 16 * s + n;
     if (row < a.Nq) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const v4f o = oacc[dt][s] * inv;
-        store4<TO>(obase + row * a.so[2] + 16 * dt + 4 * g, o.x, o.y, o.z, o.w);
+        store4<TO>(obase + (uint32_t)(row * a.son + 16 * dt + 4 * g), o.x, o.y, o.z, o.w);
       }
     }
   }
 }
 
-template <int D, typename TV, typename PV>
-static int launch_attn(const AttnArgs& a, hipStream_t st) {
-  constexpr int NW = 8, QW = 32, BM = NW * QW;
+template <int D, int NW, int QW, int SUB, typename TV, typename PV>
+static int launch_cfg(const AttnArgs& a, hipStream_t st) {
+  constexpr int BM = NW * QW;
   const int64_t nqb = (a.Nq + BM - 1) / BM;
   const int64_t grid = nqb * a.Hq * a.B;
   if (grid > 0x7FFFFFFF) return fail("sage_attn_fwd: invalid argument: grid too large");
-  hipLaunchKernelGGL((attn_fwd_kernel<D, NW, QW, TV, PV, TV>), dim3((unsigned)grid), dim3(NW * 64), 0, st, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, NW, QW, SUB, TV, PV, TV>), dim3((unsigned)grid), dim3(NW * 64), 0, st,
+                     a);
   return check_launch("sage_attn_fwd");
+}
+
+// Tiling variant: 0 = 8 waves x 32 rows, 64 keys per iteration (default);
+// 1 = 8 waves x 32 rows, 128 keys per iteration.  SAGE_ATTN_VARIANT selects.
+static int attn_variant() {
+  static int v = [] {
+    const char* e = getenv("SAGE_ATTN_VARIANT");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+template <int D, typename TV, typename PV>
+static int launch_attn(const AttnArgs& a, hipStream_t st) {
+  if (attn_variant() == 1) return launch_cfg<D, 8, 32, 2, TV, PV>(a, st);
+  return launch_cfg<D, 8, 32, 1, TV, PV>(a, st);
 }
 
 template <typename TV, typename PV>
@@ -379,7 +520,8 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   if (Hq % Hkv != 0) return fail("sage_attn_fwd: invalid argument: Hq %% Hkv != 0");
   if (Nq > 0x7FFFFFFF || Nkv > 0x7FFFFFFF || Hq > 0xFFFF || B > 0xFFFF)
     return fail("sage_attn_fwd: invalid argument: shape too large");
-  if (blkk < 64 || blkk % 64 != 0) return fail("sage_attn_fwd: invalid argument: blkk=%d (multiple of 64)", blkk);
+  if (blkk != 64 && blkk != 128 && blkk != 256)
+    return fail("sage_attn_fwd: invalid argument: blkk=%d (64, 128 or 256)", blkk);
   if (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0)
     return fail("sage_attn_fwd: invalid argument: q_sub=%d blkq=%d", q_sub, blkq);
   if (!q8 || !q_scale || !k8 || !k_scale || !v || !o || !q8_strides || !k8_strides || !v_strides || !o_strides)
@@ -389,6 +531,9 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16)
     return fail("sage_attn_fwd: invalid argument: pv_mode %d not available", pv_mode);
   const int es = v_dtype == SAGE_DTYPE_F32 ? 4 : 2;
+  const bool rows32 = Nq * q8_strides[2] + D < 0x7FFFFFFF && Nkv * k8_strides[2] + D < 0x7FFFFFFF &&
+                      Nkv * v_strides[2] + D < 0x7FFFFFFF && Nq * o_strides[2] + D < 0x7FFFFFFF;
+  if (!rows32) return fail("sage_attn_fwd: invalid argument: a head's rows must span < 2^31 elements");
   if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(v_strides, es) ||
       !strides_ok(o_strides, es))
     return fail("sage_attn_fwd: invalid argument: strides must keep 16-byte aligned rows");
@@ -403,12 +548,16 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   a.v = v;
   a.v_scale = v_scale;
   a.o = o;
-  for (int i = 0; i < 3; ++i) {
+  for (int i = 0; i < 2; ++i) {
     a.sq[i] = q8_strides[i];
     a.sk[i] = k8_strides[i];
     a.sv[i] = v_strides[i];
     a.so[i] = o_strides[i];
   }
+  a.sqn = (int)q8_strides[2];
+  a.skn = (int)k8_strides[2];
+  a.svn = (int)v_strides[2];
+  a.son = (int)o_strides[2];
   a.B = (int)B;
   a.Hq = (int)Hq;
   a.Hkv = (int)Hkv;
@@ -416,7 +565,7 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   a.Nkv = (int)Nkv;
   a.causal = causal ? 1 : 0;
   a.q_sub = q_sub;
-  a.blkk = blkk;
+  a.blkk_shift = blkk == 64 ? 0 : (blkk == 128 ? 1 : 2);
   a.nqs = (int)(((Nq + blkq - 1) / blkq) * (blkq / q_sub));
   a.nks = (int)((Nkv + blkk - 1) / blkk);
   hipStream_t st = static_cast<hipStream_t>(stream);

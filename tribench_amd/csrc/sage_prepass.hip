@@ -43,36 +43,51 @@ struct PrepassArgs {
   float* pamax;  // [B, Hkv, nch, D] V channel max|v| per chunk
   int64_t nch, chunk;
   int64_t nqb, nkb;  // blocks per head
-  int64_t n_stat, n_qblk, n_kblk_a;  // role counts of launch A
+  int64_t n_stat, n_qblk_a, n_kblk_a;  // role counts of launch A
+  int64_t n_kblk_b, n_qblk_b;          // role counts of launch B (K blocks first)
 };
 
 // ---------------------------------------------------------------------------
-// One quantization block: rows [0, rows_valid) of BLK rows x D, scale per
-// q_sub rows (q_sub == BLK: one scale per block, triton_impl.py:28,33).
-// x = fp32(in) * mul (if use_mul) - km[c] (if km); tail rows count as 0.
+// max of a non-negative value over the wave: DPP steps inside each 16-lane row
+// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row
+// results via readlane.  Result is wave-uniform.
 // ---------------------------------------------------------------------------
-template <typename T, int D>
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+
+// ---------------------------------------------------------------------------
+// One quantization block: rows [0, rows_valid) of blk rows x D, scale per
+// q_sub rows (q_sub == blk: one scale per block, triton_impl.py:28,33).
+// x = fp32(in) * mul (if use_mul) - km[c] (if km); tail rows are left out of
+// the block max and not stored.  NI = 16-element items per thread
+// (blk * D / 4096, at least 1; with fewer items than threads whole waves idle).
+// ---------------------------------------------------------------------------
+template <typename T, int D, int NI>
 __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
                             int q_sub, bool use_mul, float mul, const float* km_s,
                             int8_t* __restrict__ dst, int64_t dn, float* __restrict__ scale_dst,
                             uint32_t* amax_s, float* scl_s, float* rcp_s) {
-  constexpr int CPR = D / 16;   // 16-element items per row
-  constexpr int MAXJ = D / 16;  // items per thread when blk == 256
+  constexpr int CPR = D / 16;  // 16-element items per row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int nit = blk * CPR;  // a multiple of 64: whole waves are valid or not
   const int nsub = blk / q_sub;
 
   if (tid < 16) amax_s[tid] = 0u;
-  __syncthreads();
-
-  Raw8<T> raw[MAXJ][2];
+  Raw8<T> raw[NI][2];
+  float amx[NI];
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
+  for (int j = 0; j < NI; ++j) {
     const int it = tid + kPrepassThreads * j;
-    if (it - lane >= nit) break;  // wave-uniform
     const int row = it / CPR, c = it % CPR;
-    if (row < rows_valid) {
+    if (it < nit && row < rows_valid) {
       const T* p = src + (int64_t)row * sn + c * 16;
       raw[j][0] = load8<T>(p);
       raw[j][1] = load8<T>(p + 8);
@@ -80,8 +95,13 @@ __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_vali
       raw[j][0] = zero8<T>();
       raw[j][1] = zero8<T>();
     }
+  }
+#pragma unroll
+  for (int j = 0; j < NI; ++j) {
+    const int it = tid + kPrepassThreads * j;
+    const int row = it / CPR, c = it % CPR;
     float am = 0.0f;
-    if (row < rows_valid) {  // tail rows stay out of the block max
+    if (it < nit && row < rows_valid) {  // tail rows stay out of the block max
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float x = elem<T>(raw[j][e >> 3], e & 7);
@@ -90,9 +110,25 @@ __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_vali
         am = fmaxf(am, fabsf(x));
       }
     }
-    am = wave_max(am);
-    // a wave's 64 items cover 64/CPR consecutive rows inside one sub-block
-    if (lane == 0) atomicMax(&amax_s[((it - lane) / CPR) / q_sub], __float_as_uint(am));
+    amx[j] = am;
+  }
+  __syncthreads();  // amax_s cleared
+  if (nsub == 1) {
+    float am = amx[0];
+#pragma unroll
+    for (int j = 1; j < NI; ++j) am = fmaxf(am, amx[j]);
+    const uint32_t w = wave_max_u32(__float_as_uint(am));
+    if (lane == 0) atomicMax(&amax_s[0], w);
+  } else {
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int it0 = tid - lane + kPrepassThreads * j;  // first item of this wave
+      if (it0 < nit) {                                    // wave-uniform
+        // a wave's 64 items cover 64/CPR consecutive rows inside one sub-block
+        const uint32_t w = wave_max_u32(__float_as_uint(amx[j]));
+        if (lane == 0) atomicMax(&amax_s[(it0 / CPR) / q_sub], w);
+      }
+    }
   }
   __syncthreads();
   if (tid < nsub) {
@@ -103,11 +139,10 @@ __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_vali
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < MAXJ; ++j) {
+  for (int j = 0; j < NI; ++j) {
     const int it = tid + kPrepassThreads * j;
-    if (it - lane >= nit) break;
     const int row = it / CPR, c = it % CPR;
-    if (row >= rows_valid) continue;
+    if (it >= nit || row >= rows_valid) continue;
     const int sub = row / q_sub;
     const float sc = scl_s[sub], rc = rcp_s[sub];
     const bool fast = fast_div_ok(sc);
@@ -232,7 +267,7 @@ __device__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_val
   }
 }
 
-template <typename T, int D>
+template <typename T, int D, int NI>
 __device__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, float* scl_s,
                              float* rcp_s) {
   const int64_t qb = r % a.nqb, h = (r / a.nqb) % a.Hq, b = r / (a.nqb * a.Hq);
@@ -242,11 +277,11 @@ __device__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, 
   int8_t* dst = a.q8 + b * a.sq8[0] + h * a.sq8[1] + row0 * a.sq8[2];
   const int nsub = a.blkq / a.q_sub;
   float* sdst = a.q_scale + ((b * a.Hq + h) * a.nqb + qb) * nsub;
-  quant_block<T, D>(src, a.sq[2], rows_valid, a.blkq, a.q_sub, true, a.q_mul, nullptr, dst, a.sq8[2],
-                    sdst, amax_s, scl_s, rcp_s);
+  quant_block<T, D, NI>(src, a.sq[2], rows_valid, a.blkq, a.q_sub, true, a.q_mul, nullptr, dst, a.sq8[2],
+                        sdst, amax_s, scl_s, rcp_s);
 }
 
-template <typename T, int D>
+template <typename T, int D, int NI>
 __device__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s, uint32_t* amax_s,
                              float* scl_s, float* rcp_s) {
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
@@ -255,11 +290,12 @@ __device__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s,
   const T* src = static_cast<const T*>(a.k) + b * a.sk[0] + h * a.sk[1] + row0 * a.sk[2];
   int8_t* dst = a.k8 + b * a.sk8[0] + h * a.sk8[1] + row0 * a.sk8[2];
   float* sdst = a.k_scale + (b * a.Hkv + h) * a.nkb + kb;
-  quant_block<T, D>(src, a.sk[2], rows_valid, a.blkk, a.blkk, false, 1.0f, km_s, dst, a.sk8[2], sdst,
-                    amax_s, scl_s, rcp_s);
+  quant_block<T, D, NI>(src, a.sk[2], rows_valid, a.blkk, a.blkk, false, 1.0f, km_s, dst, a.sk8[2], sdst,
+                        amax_s, scl_s, rcp_s);
 }
 
-template <typename T, int D>
+// NIQ / NIK: 16-element items per thread of a Q / K block (blk * D / 4096).
+template <typename T, int D, int NIQ, int NIK>
 __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs a) {
   __shared__ uint32_t amax_s[16];
   __shared__ float scl_s[16], rcp_s[16];
@@ -276,41 +312,53 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs 
     return;
   }
   r -= a.n_stat;
-  if (r < a.n_qblk) {
-    quant_q_role<T, D>(a, r, amax_s, scl_s, rcp_s);
+  if (r < a.n_qblk_a) {
+    quant_q_role<T, D, NIQ>(a, r, amax_s, scl_s, rcp_s);
     return;
   }
-  r -= a.n_qblk;
-  if (r < a.n_kblk_a) quant_k_role<T, D>(a, r, nullptr, amax_s, scl_s, rcp_s);
+  r -= a.n_qblk_a;
+  if (r < a.n_kblk_a) quant_k_role<T, D, NIK>(a, r, nullptr, amax_s, scl_s, rcp_s);
 }
 
-template <typename T, int D>
+template <typename T, int D, int NIQ, int NIK>
 __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs a) {
   __shared__ uint32_t amax_s[16];
   __shared__ float scl_s[16], rcp_s[16];
   __shared__ float km_s[D], vs_s[D];
   const int64_t r = blockIdx.x;
+  if (r >= a.n_kblk_b) {  // Q blocks follow the K blocks
+    quant_q_role<T, D, NIQ>(a, r - a.n_kblk_b, amax_s, scl_s, rcp_s);
+    return;
+  }
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
   const int tid = threadIdx.x;
   const int64_t base = (b * a.Hkv + h) * a.nch * D;
   if (tid < D) {
     if (a.smooth_k) {
-      float s = a.psum[base + tid];
-      for (int64_t c = 1; c < a.nch; ++c) s = s + a.psum[base + c * D + tid];
+      // issue every partial load first (nch <= 16), then add left to right
+      float part[16];
+#pragma unroll
+      for (int c = 0; c < 16; ++c) part[c] = c < a.nch ? a.psum[base + c * D + tid] : 0.0f;
+      float s = part[0];
+#pragma unroll
+      for (int c = 1; c < 16; ++c)
+        if (c < a.nch) s = s + part[c];
       const float m = s / (float)a.Nkv;
       km_s[tid] = m;
       if (kb == 0) a.km[(b * a.Hkv + h) * D + tid] = m;
     }
     if (a.v_fp8) {
       float m = a.pamax[base + tid];
-      for (int64_t c = 1; c < a.nch; ++c) m = fmaxf(m, a.pamax[base + c * D + tid]);
+#pragma unroll
+      for (int c = 1; c < 16; ++c)
+        if (c < a.nch) m = fmaxf(m, a.pamax[base + c * D + tid]);
       const float s = m / 448.0f;
       vs_s[tid] = s;
       if (kb == 0) a.v_scale[(b * a.Hkv + h) * D + tid] = s;
     }
   }
   __syncthreads();
-  quant_k_role<T, D>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
+  quant_k_role<T, D, NIK>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
   if (a.v_fp8) {
     const int64_t row0 = kb * a.blkk;
     const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
@@ -320,19 +368,28 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs 
   }
 }
 
-template <typename T, int D>
-static int launch_prepass(const PrepassArgs& a, hipStream_t st) {
-  const int64_t na = a.n_stat + a.n_qblk + a.n_kblk_a;
+template <typename T, int D, int NIQ, int NIK>
+static int launch_prepass_ni(const PrepassArgs& a, hipStream_t st) {
+  const int64_t na = a.n_stat + a.n_qblk_a + a.n_kblk_a;
   if (na > 0) {
-    hipLaunchKernelGGL((prepass_a_kernel<T, D>), dim3((unsigned)na), dim3(kPrepassThreads), 0, st, a);
+    hipLaunchKernelGGL((prepass_a_kernel<T, D, NIQ, NIK>), dim3((unsigned)na), dim3(kPrepassThreads), 0, st, a);
     if (int rc = check_launch("sage_prepass (launch A)")) return rc;
   }
-  if (a.n_kblk_a == 0) {
-    const int64_t nb = a.nkb * a.Hkv * a.B;
-    hipLaunchKernelGGL((prepass_b_kernel<T, D>), dim3((unsigned)nb), dim3(kPrepassThreads), 0, st, a);
+  if (a.n_kblk_b > 0) {
+    const int64_t nb = a.n_kblk_b + a.n_qblk_b;
+    hipLaunchKernelGGL((prepass_b_kernel<T, D, NIQ, NIK>), dim3((unsigned)nb), dim3(kPrepassThreads), 0, st, a);
     if (int rc = check_launch("sage_prepass (launch B)")) return rc;
   }
   return 0;
+}
+
+// Exact-fit kernels for the reference's block sizes (BLKQ 128, BLKK 64);
+// every other block size runs the 8-items-per-thread kernel.
+template <typename T, int D>
+static int launch_prepass(const PrepassArgs& a, hipStream_t st) {
+  constexpr int NQ = 128 * D / 4096, NK = 64 * D / 4096 > 0 ? 64 * D / 4096 : 1;
+  if (a.blkq == 128 && a.blkk == 64) return launch_prepass_ni<T, D, NQ, NK>(a, st);
+  return launch_prepass_ni<T, D, 8, 8>(a, st);
 }
 
 static bool strides_ok(const int64_t* s, int esize) {
@@ -437,10 +494,15 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   a.nqb = (Nq + blkq - 1) / blkq;
   a.nkb = (Nkv + blkk - 1) / blkk;
   const bool need_b = a.smooth_k || a.v_fp8;
+  // Launch A computes the K statistics; launch B then quantizes K (re-read
+  // while it is likely still in the Infinity Cache) and Q.  Without
+  // statistics everything runs in launch A.
   a.n_stat = need_b ? a.nch * Hkv * B : 0;
-  a.n_qblk = a.nqb * Hq * B;
+  a.n_qblk_a = need_b ? 0 : a.nqb * Hq * B;
   a.n_kblk_a = need_b ? 0 : a.nkb * Hkv * B;
-  if (a.n_stat + a.n_qblk + a.n_kblk_a > 0x7FFFFFFF || a.nkb * Hkv * B > 0x7FFFFFFF)
+  a.n_kblk_b = need_b ? a.nkb * Hkv * B : 0;
+  a.n_qblk_b = need_b ? a.nqb * Hq * B : 0;
+  if (a.n_stat + a.n_qblk_a + a.n_kblk_a > 0x7FFFFFFF || a.n_kblk_b + a.n_qblk_b > 0x7FFFFFFF)
     return fail("sage_prepass: invalid argument: grid too large");
 
   hipStream_t st = static_cast<hipStream_t>(stream);

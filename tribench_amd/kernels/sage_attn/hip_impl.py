@@ -194,6 +194,15 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
     return out
 
 
+def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
+                  tensor_layout="HND", **kw):
+    """The pre-pass of :func:`run` alone, with run's arguments (the harness
+    times it as the ``prepass`` stage to report its HBM rate)."""
+    q_sub = WAVE_ROWS if q_gran == "wave" else 128
+    return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, v_fp8=pv_dtype == "fp8",
+                   tensor_layout=tensor_layout)
+
+
 def per_block_int8(q, k, km=None, BLKQ=128, BLKK=64, sm_scale=None, tensor_layout="HND"):
     """HIP counterpart of per_block_int8 (triton_impl.py:35-82).
 
@@ -204,6 +213,33 @@ def per_block_int8(q, k, km=None, BLKQ=128, BLKK=64, sm_scale=None, tensor_layou
         k = k - km
     r = prepass(q, k, k, sm_scale, blkq=BLKQ, blkk=BLKK, smooth_k=False, tensor_layout=tensor_layout)
     return r["q8"], r["q_scale"], r["k8"], r["k_scale"]
+
+
+def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=128, blkk=64, tensor_layout="HND",
+              out=None):
+    """Launch the fused attention kernel on the outputs of :func:`prepass`.
+
+    Replaces the _attn_fwd launch of triton_impl.py:186-199.  Returns o with
+    q's shape and dtype (written into ``out`` when given).
+    """
+    lib = _load()
+    if pv_dtype not in PV_MODES:
+        raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
+    B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
+    o = _empty_like_layout(q, q.dtype) if out is None else out
+    if pv_dtype == "fp8":
+        v_in, v_code, v_str = pre["v8"], DTYPE_FP8E4M3, _strides(pre["v8"], tensor_layout)
+    else:
+        v_in, v_code, v_str = v, _TORCH_CODES[v.dtype], _strides(v, tensor_layout)
+    rc = lib.sage_attn_fwd(
+        _ptr(pre["q8"]), _strides(pre["q8"], tensor_layout), _ptr(pre["q_scale"]),
+        _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
+        _ptr(v_in), v_code, v_str, _ptr(pre.get("v_scale")),
+        _ptr(o), _TORCH_CODES[o.dtype], _strides(o, tensor_layout),
+        B, Hq, Hkv, Nq, Nkv, D, int(bool(causal)), blkq, blkk, q_sub, PV_MODES[pv_dtype], _stream(q.device),
+    )
+    _check(rc, "sage_attn_fwd")
+    return o
 
 
 def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
@@ -221,30 +257,17 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
                32 rows (the attention kernel's per-wavefront tile)
     smooth_k   subtract the per-channel K mean before quantizing (default on)
     """
-    lib = _load()
     if pv_dtype not in PV_MODES:
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
     if q_gran not in ("block", "wave"):
         raise ValueError(f"sage_attn hip: invalid argument: q_gran {q_gran!r}")
-    B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
+    _check_inputs(q, k, v, tensor_layout)
     blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
     q_sub = WAVE_ROWS if q_gran == "wave" else blkq
-    v_fp8 = pv_dtype == "fp8"
-    pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k, v_fp8=v_fp8,
+    pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k,
+                  v_fp8=pv_dtype == "fp8", tensor_layout=tensor_layout)
+    o = attention(q, k, v, pre, causal, pv_dtype=pv_dtype, q_sub=q_sub, blkq=blkq, blkk=blkk,
                   tensor_layout=tensor_layout)
-    o = _empty_like_layout(q, q.dtype)
-    if v_fp8:
-        v_in, v_code, v_str = pre["v8"], DTYPE_FP8E4M3, _strides(pre["v8"], tensor_layout)
-    else:
-        v_in, v_code, v_str = v, _TORCH_CODES[v.dtype], _strides(v, tensor_layout)
-    rc = lib.sage_attn_fwd(
-        _ptr(pre["q8"]), _strides(pre["q8"], tensor_layout), _ptr(pre["q_scale"]),
-        _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
-        _ptr(v_in), v_code, v_str, _ptr(pre.get("v_scale")),
-        _ptr(o), _TORCH_CODES[o.dtype], _strides(o, tensor_layout),
-        B, Hq, Hkv, Nq, Nkv, D, int(bool(causal)), blkq, blkk, q_sub, PV_MODES[pv_dtype], _stream(q.device),
-    )
-    _check(rc, "sage_attn_fwd")
     if return_intermediates:
         pre.pop("workspace", None)
         return o, pre
