@@ -1,0 +1,92 @@
+"""The C-ABI library on a host without a GPU: it loads, exports every symbol
+of include/sage_attn.h, and rejects bad arguments before touching a device."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sage_attn.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sage_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib(hip_impl):
+    return hip_impl._load()
+
+
+def test_header_declares_the_entry_points():
+    assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_last_error", "sage_prepass",
+                                     "sage_prepass_workspace_bytes"]
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_matches_header(lib, hip_impl):
+    m = re.search(r"#define SAGE_ABI_VERSION (\d+)", HEADER.read_text())
+    assert lib.sage_abi_version() == int(m.group(1)) == hip_impl.ABI_VERSION
+
+
+def test_workspace_bytes(lib):
+    # smooth_k: B*Hkv*nch*D fp32 partial sums; FP8 V adds as many channel maxima
+    nch = 16  # N = 4096 -> 16 chunks of 256 tokens
+    assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 1, 0) == 4 * 32 * nch * 128 * 4
+    assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 1, 1) == 2 * 4 * 32 * nch * 128 * 4
+    assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 0, 0) == 0
+
+
+def _prepass_args(**over):
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    a = dict(q=ctypes.c_void_p(16), k=ctypes.c_void_p(16), v=None, in_dtype=2, B=1, Hq=2, Hkv=2, Nq=64, Nkv=64,
+             D=64, qs=s3, ks=s3, vs=None, mul=0.18, blkq=128, blkk=64, q_sub=128, smooth=0, vmode=0,
+             q8=ctypes.c_void_p(16), q8s=s3, qsc=ctypes.c_void_p(16), k8=ctypes.c_void_p(16), k8s=s3,
+             ksc=ctypes.c_void_p(16), km=None, v8=None, v8s=None, vsc=None, ws=None, wsb=0, st=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,needle", [
+    (dict(D=96), "head_dim"),
+    (dict(Hq=3, Hkv=2), "multiple"),
+    (dict(B=0), "empty shape"),
+    (dict(blkq=100), "blkq"),
+    (dict(q_sub=48), "q_sub"),
+    (dict(in_dtype=7), "in_dtype"),
+    (dict(smooth=1), "km is null"),
+    (dict(q=None), "null pointer"),
+    (dict(q=ctypes.c_void_p(8)), "aligned"),
+])
+def test_prepass_rejects_bad_arguments(lib, over, needle):
+    rc = lib.sage_prepass(*_prepass_args(**over))
+    msg = lib.sage_last_error().decode()
+    assert rc != 0 and "invalid argument" in msg and needle in msg, msg
+
+
+def test_attn_rejects_bad_arguments(lib):
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    p = ctypes.c_void_p(16)
+    rc = lib.sage_attn_fwd(p, s3, p, p, s3, p, p, 2, s3, None, p, 2, s3, 1, 2, 2, 64, 64, 64, 0, 128, 32, 128, 0,
+                           None)
+    assert rc != 0 and "blkk" in lib.sage_last_error().decode()
+    rc = lib.sage_attn_fwd(p, s3, p, p, s3, p, p, 2, s3, None, p, 1, s3, 1, 2, 2, 64, 64, 64, 0, 128, 64, 128, 0,
+                           None)
+    assert rc != 0 and "v_dtype" in lib.sage_last_error().decode()
+
+
+def test_hip_variant_refuses_cpu_tensors(hip_impl):
+    import torch
+
+    q = torch.zeros(1, 2, 16, 64)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        hip_impl.run(q, q, q)

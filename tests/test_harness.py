@@ -1,0 +1,277 @@
+"""The harness around the hot path, on the CPU: schema, registry, case grid,
+inputs, reference, correctness gate, timers, metrics, CLI and outputs.
+
+Schema tests follow the reference's tests/test_meta_schema.py (:12-134); the
+CLI failure handling is forced from the host with fake packs (an impl that
+raises, an impl that returns wrong values), as the reference's CLI handles
+them (cli.py:313-339).
+"""
+from __future__ import annotations
+
+import copy
+import json
+import math
+import textwrap
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sage_oracle as O
+from tribench_amd.harness import bench as hb
+from tribench_amd.harness import cli
+from tribench_amd.harness.correctness import _get_tolerance, check_correctness
+from tribench_amd.harness.gen import generate_cases, materialize_inputs
+from tribench_amd.harness.meta import load_meta, validate_entrypoints, validate_meta
+from tribench_amd.harness.metrics import PEAKS_MI355X, compute_gbps, compute_tflops, roofline_fraction
+from tribench_amd.harness.registry import KernelRegistry
+from tribench_amd.harness.types import CorrectnessSpec
+
+VALID_META = {
+    "schema_version": "1.0",
+    "name": "test_kernel",
+    "family": "test",
+    "description": "A test kernel",
+    "entrypoints": {"make_inputs": "reference.py:make_inputs", "reference": "reference.py:ref",
+                    "variants": {"hip": "impl.py:run"}},
+    "supported": {"dtypes": ["fp16", "bf16"], "layouts": ["contiguous"], "backends": ["hip"]},
+    "cases": [{"name": "small", "N": 16}],
+}
+
+
+# ---------------------------------------------------------------------------
+# schema
+# ---------------------------------------------------------------------------
+
+def test_valid_meta_passes():
+    assert validate_meta(VALID_META) == []
+
+
+@pytest.mark.parametrize("field", ["schema_version", "name", "family", "description", "entrypoints", "supported",
+                                   "cases"])
+def test_missing_top_field(field):
+    m = copy.deepcopy(VALID_META)
+    del m[field]
+    assert any(field in e for e in validate_meta(m))
+
+
+@pytest.mark.parametrize("path,value,needle", [
+    (("supported", "dtypes"), ["fp8"], "Invalid dtype"),
+    (("supported", "layouts"), ["strided"], "Invalid layout"),
+    (("supported", "backends"), ["metal"], "Invalid backend"),
+    (("entrypoints", "variants"), ["x"], "must be a dict"),
+])
+def test_bad_values(path, value, needle):
+    m = copy.deepcopy(VALID_META)
+    m[path[0]][path[1]] = value
+    assert any(needle in e for e in validate_meta(m))
+
+
+def test_case_without_name_and_bad_schema_version():
+    m = copy.deepcopy(VALID_META)
+    m["cases"] = [{"N": 3}]
+    m["schema_version"] = 1
+    errs = validate_meta(m)
+    assert any("missing 'name'" in e for e in errs) and any("must be a string" in e for e in errs)
+
+
+def test_pack_needs_an_implementation():
+    m = copy.deepcopy(VALID_META)
+    m["entrypoints"].pop("variants")
+    assert any("No implementation" in e for e in validate_meta(m))
+    m["entrypoints"]["triton"] = "impl.py:run"  # a reference-style main entrypoint also counts
+    assert validate_meta(m) == []
+
+
+def test_sage_pack_meta_and_entrypoints():
+    reg = KernelRegistry()
+    assert "sage_attn" in reg.kernel_names()
+    assert reg.validate_all() == {}
+    meta = reg.get_meta("sage_attn")
+    assert meta.entrypoints.variants == {"hip": "hip_impl.py:run"}
+    assert validate_entrypoints(meta) == []
+    names = [c.name for c in meta.cases]
+    assert {"s4k_d64", "s8k_d64", "cfg1_b1h2n256d64", "cfg2_b4h32n4096d128"} <= set(names)
+
+
+# ---------------------------------------------------------------------------
+# registry / case grid / inputs / reference / estimate
+# ---------------------------------------------------------------------------
+
+def test_registry_loads_by_file_path_without_a_parent_package():
+    reg = KernelRegistry()
+    impls = reg.implementations("sage_attn")
+    assert [n for n, _ in impls] == ["hip"]
+    fn = impls[0][1]
+    assert fn.__module__ == "tribench.kernels.sage_attn.hip_impl"
+
+
+def test_generate_cases_grid_and_filters():
+    meta = KernelRegistry().get_meta("sage_attn")
+    grid = generate_cases(meta, case_filter=["cfg2_b4h32n4096d128"], dtype_filter=["bf16"])
+    assert len(grid) == 1 and grid[0]["params"]["head_dim"] == 128 and grid[0]["dtype"] == "bf16"
+    assert len(generate_cases(meta)) == len(meta.cases) * 3
+    with pytest.raises(ValueError, match="does not support dtype"):
+        generate_cases(meta, dtype_filter=["fp64"])
+    with pytest.raises(ValueError, match="no case"):
+        generate_cases(meta, case_filter=["nope"])
+
+
+def test_materialize_inputs_is_seeded(pack_ref):
+    case = {"case_name": "c", "params": dict(batch_size=1, num_heads=2, num_kv_heads=1, seq_len=40, head_dim=64,
+                                             k_offset_std=2.0), "dtype": "bf16", "layout": "contiguous"}
+    a = materialize_inputs(pack_ref.make_inputs, case, "cpu", 0)
+    b = materialize_inputs(pack_ref.make_inputs, case, "cpu", 0)
+    c = materialize_inputs(pack_ref.make_inputs, case, "cpu", 1)
+    assert all(torch.equal(a[x], b[x]) for x in "qkv") and not torch.equal(a["q"], c["q"])
+    assert a["q"].shape == (1, 2, 40, 64) and a["k"].shape == (1, 1, 40, 64) and a["q"].dtype == torch.bfloat16
+
+
+def test_make_inputs_distributions(pack_ref):
+    base = dict(batch_size=2, num_heads=2, seq_len=4000, head_dim=64)
+    plain = pack_ref.make_inputs(base, "cpu", 0, torch.float32)
+    off = pack_ref.make_inputs(dict(base, k_offset_std=2.0), "cpu", 0, torch.float32)
+    d = off["k"] - plain["k"]  # the offset is constant over tokens
+    assert torch.allclose(d, d[:, :, :1].expand_as(d), atol=1e-5) and 0.5 < d[:, :, 0].std() < 4
+    assert torch.equal(off["q"], plain["q"]) and torch.equal(off["v"], plain["v"])
+    st = pack_ref.make_inputs(dict(base, v_dist="student_t", v_df=3), "cpu", 0, torch.float32)
+    kurt = lambda x: float(((x - x.mean()) ** 4).mean() / x.var() ** 2)  # noqa: E731
+    assert kurt(st["v"]) > 6 > kurt(plain["v"])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_pack_reference_matches_oracle(pack_ref, causal):
+    inp = pack_ref.make_inputs(dict(batch_size=1, num_heads=4, num_kv_heads=2, seq_len=70, head_dim=64),
+                               "cpu", 3, torch.float32)
+    got = pack_ref.ref(inp["q"], inp["k"], inp["v"], causal=causal, q_chunk=32)
+    want = O.sdpa(inp["q"].numpy(), inp["k"].numpy(), inp["v"].numpy(), causal=causal)
+    assert got.dtype == torch.float32 and np.abs(got.numpy() - want).max() < 1e-5
+
+
+def test_estimate(pack_ref):
+    e = pack_ref.estimate(dict(batch_size=4, num_heads=32, seq_len=4096, head_dim=128))
+    assert e["flops"] == e["algo_flops"] == 2 ** 40 and e["bytes"] == 4 * 4 * 32 * 4096 * 128 * 2
+    assert abs(e["prepass_bytes"] / 402.8e6 - 1) < 1e-3
+    c = pack_ref.estimate(dict(batch_size=2, num_heads=32, seq_len=16384, head_dim=128, causal=True))
+    assert c["flops"] == 2 ** 43 and c["algo_flops"] == O.attention_flops(2, 32, 16384, 16384, 128, True)[1]
+
+
+# ---------------------------------------------------------------------------
+# correctness gate / metrics
+# ---------------------------------------------------------------------------
+
+def test_tolerance_precedence():
+    assert _get_tolerance("bf16", CorrectnessSpec()) == (1e-2, 1e-2)
+    assert _get_tolerance("fp32", CorrectnessSpec()) == (1e-5, 1e-4)
+    assert _get_tolerance("bf16", CorrectnessSpec(atol=5e-2, rtol=5e-2)) == (5e-2, 5e-2)
+    spec = CorrectnessSpec(atol=5e-2, rtol=5e-2, per_dtype={"fp16": {"atol": 1e-3}})
+    assert _get_tolerance("fp16", spec) == (1e-3, 5e-2)
+
+
+def test_check_correctness_reports_cosine_and_bounds():
+    ref = torch.randn(1000, generator=torch.Generator().manual_seed(0))
+    res = check_correctness(ref, ref + 1e-3, "bf16", CorrectnessSpec(atol=5e-2, rtol=5e-2, max_abs=2e-2,
+                                                                   min_cos=0.999))
+    assert res.passed and abs(res.max_abs_err - 1e-3) < 1e-6 and res.cosine > 0.9999
+    bad = check_correctness(ref, ref + 3e-2, "bf16", CorrectnessSpec(atol=5e-2, rtol=5e-2, max_abs=2e-2))
+    assert not bad.passed and "max_abs" in bad.error_msg
+    neg = check_correctness(ref, -ref, "bf16", CorrectnessSpec(atol=10, rtol=0, min_cos=0.999))
+    assert not neg.passed and neg.cosine < -0.99
+    assert not check_correctness(ref, ref[:10], "bf16", CorrectnessSpec()).passed
+    assert check_correctness([ref, ref], [ref, ref], "bf16", CorrectnessSpec()).passed
+
+
+def test_metrics():
+    assert compute_tflops(1e12, 1.0) == 1000.0 and compute_gbps(8e9, 1.0) == 8000.0
+    assert compute_tflops(1.0, 0.0) == 0.0
+    assert roofline_fraction(2500.0, "int8") == pytest.approx(2500 / PEAKS_MI355X["int8"])
+    assert PEAKS_MI355X["hbm_gbps"] == 8000.0
+
+
+# ---------------------------------------------------------------------------
+# timers, fake packs, CLI
+# ---------------------------------------------------------------------------
+
+def _fake_pack(root: Path, impl_body: str) -> Path:
+    d = root / "kernels" / "fake"
+    d.mkdir(parents=True)
+    meta = copy.deepcopy(VALID_META)
+    meta["name"] = "fake"
+    meta["supported"]["dtypes"] = ["fp32"]
+    meta["entrypoints"]["estimate"] = "reference.py:estimate"
+    meta["correctness"] = {"atol": 1e-5, "rtol": 1e-5}
+    (d / "meta.json").write_text(json.dumps(meta))
+    (d / "reference.py").write_text(textwrap.dedent("""
+        import torch
+        def make_inputs(case, device, seed, dtype, **kw):
+            g = torch.Generator().manual_seed(seed)
+            return {"x": torch.randn(case["N"], generator=g).to(dtype).to(device)}
+        def ref(x):
+            return x * 2
+        def estimate(case):
+            return {"flops": 2 * case["N"], "bytes": 8 * case["N"]}
+    """))
+    (d / "impl.py").write_text(textwrap.dedent(impl_body))
+    return root / "kernels"
+
+
+@pytest.mark.parametrize("body,code,needle", [
+    ("def run(x):\n    return x * 2\n", 0, "PASS"),
+    ("def run(x):\n    return x * 3\n", 1, "FAIL"),
+    ("def run(x):\n    raise RuntimeError('sage_attn hip: invalid argument: shape')\n", 1, "Shape mismatch"),
+])
+def test_cli_test_on_fake_packs(tmp_path, monkeypatch, capsys, body, code, needle):
+    kdir = _fake_pack(tmp_path, body)
+    monkeypatch.setattr("tribench_amd.harness.registry._DEFAULT_KERNELS_DIR", kdir)
+    with pytest.raises(SystemExit) as e:
+        cli.main(["test", "--kernel", "fake", "--device", "cpu"])
+    out = capsys.readouterr().out
+    assert e.value.code == code and needle in out
+
+
+def test_cli_test_hip_variant_without_gpu_fails_loudly(capsys):
+    with pytest.raises(SystemExit) as e:
+        cli.main(["test", "--kernel", "sage_attn", "--cases", "cfg1_b1h2n256d64", "--dtype", "fp32",
+                  "--device", "cpu"])
+    out = capsys.readouterr().out
+    assert e.value.code == 1 and "FAIL" in out and "ROCm GPU device" in out
+
+
+def test_cli_run_writes_results(tmp_path, monkeypatch, capsys):
+    kdir = _fake_pack(tmp_path, "def run(x):\n    return x * 2\n")
+    monkeypatch.setattr("tribench_amd.harness.registry._DEFAULT_KERNELS_DIR", kdir)
+    with pytest.raises(SystemExit) as e:
+        cli.main(["run", "--kernel", "fake", "--device", "cpu", "--timer", "cpu_wall", "--warmup-ms", "1",
+                  "--rep-ms", "5", "--output-dir", str(tmp_path / "res"), "--cpu-ref"])
+    assert e.value.code == 0
+    runs = list((tmp_path / "res").glob("*/run.json"))
+    assert len(runs) == 1
+    rec = json.loads(runs[0].read_text())
+    rows = rec["results"]
+    assert rows[0]["variant"] == "hip" and rows[0]["correctness"]["passed"] and rows[0]["effective_tops"] > 0
+    assert rows[1]["variant"] == "cpu_ref" and rows[1]["cpu_threads"] >= 1
+    assert (runs[0].parent / "summary.md").exists()
+
+
+def test_cli_list_and_validate(capsys):
+    with pytest.raises(SystemExit) as e:
+        cli.main(["validate-meta"])
+    assert e.value.code == 0
+    with pytest.raises(SystemExit) as e:
+        cli.main(["list"])
+    assert e.value.code == 0 and "sage_attn" in capsys.readouterr().out
+
+
+def test_cpu_timer_and_stats():
+    lats = hb._bench_cpu_wall(lambda: math.sqrt(2.0), 1.0, 2.0)
+    st = hb._stats(lats)
+    assert len(lats) >= 1 and st["p50"] >= 0 and st["p99"] >= st["p50"]
+    threads, model = hb.cpu_info()
+    assert threads >= 1 and isinstance(model, str)
+
+
+def test_load_meta_keeps_case_params():
+    meta = load_meta(Path(KernelRegistry().get_meta("sage_attn").kernel_dir) / "meta.json")
+    c = {x.name: x.params for x in meta.cases}["cfg5_fp8pv_b1h32n32768d128"]
+    assert c["pv_dtype"] == "fp8" and c["q_gran"] == "wave" and "name" not in c
