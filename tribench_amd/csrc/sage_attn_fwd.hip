@@ -1,37 +1,55 @@
 // sage_attn_fwd.hip — fused SageAttention forward for gfx950 (MI355X).
 //
 // Replaces _attn_fwd / _attn_fwd_inner (kernels/sage_attn/triton_impl.py:86-160)
-// and its launch (:186-199).  Per key block of 64:
-//   S^T = K8 . Q8^T            v_mfma_i32_16x16x64_i8   (INT8, i32 accumulate)
+// and its launch (:186-199).  Per block of 64 keys:
+//   S^T = K8 . Q8^T          v_mfma_i32_32x32x32_i8 (INT8, i32 accumulate)
 //   s   = float(S) * (q_scale * k_scale)          (triton_impl.py:99)
 //   online base-2 softmax: m, l, p = exp2(s - m)   (triton_impl.py:102-109)
-//   O^T += V^T . P^T           v_mfma_f32_16x16x32_{f16,bf16}, fp32 accumulate
-// and O / l at the end (triton_impl.py:159).  Causal (top-left, like the
-// torch.tril mask of reference.py:19-22), ragged tails and GQA
-// (kv head = h / (Hq/Hkv), triton_impl.py:137,145,147) are handled here; the
-// reference kernel ignores `causal`.
+//   O^T += V^T . P^T         v_mfma_f32_32x32x16_{f16,bf16}, or FP8 e4m3
+//                            v_mfma_f32_32x32x64_f8f6f4; fp32 accumulate
+// and O / l at the end (triton_impl.py:159).  Causal (top-left, the torch.tril
+// mask of reference.py:19-22), ragged tails and GQA (kv head = h / (Hq/Hkv),
+// triton_impl.py:137,145,147) are handled here.
 //
-// Layout choices (CDNA4):
-//  * The score tile is computed transposed, S^T[key][q].  Its MFMA C layout
-//    (lane = 16*g + n holds q = n and keys 4g..4g+3 of a 16-key tile) is, after
-//    conversion to 16 bit, exactly the B-operand layout of the P.V MFMA, so P
-//    never leaves registers.  Row max and row sum are per lane plus two xor
-//    shuffles across the four lane groups.
-//  * K8 tiles live in LDS row-major with 16-byte chunks XOR-swizzled by the
-//    128-byte line index (conflict-free ds_read_b128 for the A operand).
-//  * V tiles are converted to the P.V type while being staged and stored
-//    transposed (V^T[d][key], 8-byte chunks swizzled) so each lane's A operand
-//    is two ds_read_b64.
-//  * K/V tiles are double-buffered: global loads for block j+1 are in flight
-//    while block j is computed; one barrier per block.
-//  * Work-group ids are remapped so that all q-blocks of one (batch, kv head)
-//    run on the same XCD (shared L2) — the hardware deals work-groups to the 8
-//    XCDs round-robin.
+// Organisation (CDNA4):
+//  * A work-group covers 256 query rows of one (batch, head).  The launched
+//    shape is 8 waves (2 per SIMD) of 32 rows each (one 32-row MFMA tile,
+//    QT = 1): Q8 rows, S, P and the O^T accumulators (fp32, 32 x D) all live
+//    in arch VGPRs.  The kernel also builds as 4 waves of 64 rows (QT = 2, O
+//    in the accumulation registers, Q8 read from LDS), which halves LDS
+//    operand traffic but leaves the compiler copying accumulators between
+//    register files.
+//  * K8 and V^T tiles of 64 keys are staged through LDS for all the waves:
+//    the loads of tile j+2 are issued at the top of iteration j and written to
+//    LDS at its end (2 K buffers, 4 V^T buffers, one barrier per iteration).
+//    V is transposed (and converted to the P.V type) while staged.
+//  * Software pipeline inside each wave: iteration j runs the P.V MFMAs of
+//    block j-1 together with the softmax of block j (VALU), then the QK MFMAs
+//    of block j+1, so the matrix cores and the vector ALUs work at the same
+//    time.  Blocks that need no mask take a path with no masking code.
+//  * The i32 score accumulator starts at the bit pattern of 2^23 + 2^22, so
+//    it reads as the float 12582912 + S (exact for |S| < 2^22 >= 127^2 * D):
+//    dequantisation and max-subtraction are one FMA per score.
+//  * Lazy rescale: the running max moves only when a block's max exceeds it
+//    by more than tau (log2 units), so P stays bounded (SoftmaxCfg); the O
+//    rescale that a move needs is applied at the start of the next
+//    iteration, once the P.V MFMAs of the previous block have retired.
+//  * The MFMA C layout (lane 32h + n holds column n, rows 8i + 4h + r) is used
+//    as the B operand of the P.V product directly: P never leaves
+//    registers.  V^T columns are stored in LDS in the order in which a lane
+//    half holds the keys, so each A operand is one or two ds_read_b128.
+//  * Work-group ids are remapped so that all q-blocks of one (batch, head)
+//    run on one XCD (shared L2): the hardware deals work-groups to the 8 XCDs
+//    round-robin.
 #include <stdlib.h>
 
 #include "sage_device.h"
 
 namespace sage {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct AttnArgs {
   const int8_t* q8;
@@ -49,32 +67,70 @@ struct AttnArgs {
   int nqs, nks;           // q / k scales per head
 };
 
-template <typename P>
-struct PvOps;
+constexpr int kBM = 256;  // query rows per work-group
+constexpr int kBN = 64;   // keys per block
+constexpr int kKBuf = 2, kVBuf = 4;
+
+// The int32 MFMA accumulator starts at the bit pattern of 2^23 + 2^22.
+constexpr int kMagicI = 0x4B400000;
+constexpr float kMagicF = 12582912.0f;
+
+// Lazy rescale threshold (log2 units) and the power of two P is scaled by
+// before rounding to the P.V type.  fp16/bf16: P = 2^(s-m) <= 2^8.  FP8 e4m3
+// (normal from 2^-6, max 448): P = 2^(s-m+6) <= 2^8 with tau = 2, so every
+// score within 12 of the running max rounds to a normal number.  The row
+// sums use the same scaled P, so the scale cancels in O / l.
+template <int M>
+struct SoftmaxCfg {
+  static constexpr float kTau = 8.0f, kShift = 0.0f;
+};
 template <>
-struct PvOps<_Float16> {
-  typedef v8h V8;
-  __device__ static __forceinline__ v4i ones() { return (v4i){0x3C003C00, 0x3C003C00, 0x3C003C00, 0x3C003C00}; }
+struct SoftmaxCfg<SAGE_PV_FP8> {
+  static constexpr float kTau = 2.0f, kShift = 6.0f;
+};
+
+// ---------------------------------------------------------------------------
+// P.V operand types
+// ---------------------------------------------------------------------------
+template <int M>
+struct PvT;
+template <>
+struct PvT<SAGE_PV_F16> {
+  static constexpr int kEB = 2;   // bytes per V^T element in LDS
+  static constexpr int kPW = 16;  // P dwords per lane per (block, q tile)
   __device__ static __forceinline__ uint32_t pack2(float a, float b) {
-    h2 r = __builtin_convertvector((f2){a, b}, h2);
-    return __builtin_bit_cast(uint32_t, r);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, h2));
   }
-  __device__ static __forceinline__ v4f mfma(const v4i& a, const v4i& b, const v4f& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0,
-                                                  0, 0);
+  __device__ static __forceinline__ v16f mma(const v4i& a, const v4i& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a), __builtin_bit_cast(v8h, b), c, 0, 0,
+                                                  0);
   }
 };
 template <>
-struct PvOps<__bf16> {
-  typedef v8bf V8;
-  __device__ static __forceinline__ v4i ones() { return (v4i){0x3F803F80, 0x3F803F80, 0x3F803F80, 0x3F803F80}; }
+struct PvT<SAGE_PV_BF16> {
+  static constexpr int kEB = 2;
+  static constexpr int kPW = 16;
   __device__ static __forceinline__ uint32_t pack2(float a, float b) {
-    bf2 r = __builtin_convertvector((f2){a, b}, bf2);
-    return __builtin_bit_cast(uint32_t, r);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){a, b}, bf2));
   }
-  __device__ static __forceinline__ v4f mfma(const v4i& a, const v4i& b, const v4f& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c,
-                                                   0, 0, 0);
+  __device__ static __forceinline__ v16f mma(const v4i& a, const v4i& b, const v16f& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a), __builtin_bit_cast(v8bf, b), c, 0,
+                                                   0, 0);
+  }
+};
+template <>
+struct PvT<SAGE_PV_FP8> {
+  static constexpr int kEB = 1;
+  static constexpr int kPW = 8;
+  // two fp32 -> two OCP e4m3 bytes (round to nearest even) in the low or high half
+  __device__ static __forceinline__ uint32_t pack4(float a, float b, float c, float d) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+    return (uint32_t)w;
+  }
+  __device__ static __forceinline__ v16f mma(const v8i& a, const v8i& b, const v16f& c) {
+    // format 0 (e4m3) for both operands, unit E8M0 scales (127 = 2^0)
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
   }
 };
 
@@ -86,78 +142,93 @@ __device__ __forceinline__ void store4<float>(float* p, float a, float b, float 
 }
 template <>
 __device__ __forceinline__ void store4<_Float16>(_Float16* p, float a, float b, float c, float d) {
-  v2i w = {(int)PvOps<_Float16>::pack2(a, b), (int)PvOps<_Float16>::pack2(c, d)};
+  v2i w = {(int)PvT<SAGE_PV_F16>::pack2(a, b), (int)PvT<SAGE_PV_F16>::pack2(c, d)};
   *reinterpret_cast<v2i*>(p) = w;
 }
 template <>
 __device__ __forceinline__ void store4<__bf16>(__bf16* p, float a, float b, float c, float d) {
-  v2i w = {(int)PvOps<__bf16>::pack2(a, b), (int)PvOps<__bf16>::pack2(c, d)};
+  v2i w = {(int)PvT<SAGE_PV_BF16>::pack2(a, b), (int)PvT<SAGE_PV_BF16>::pack2(c, d)};
   *reinterpret_cast<v2i*>(p) = w;
 }
 
-// ---------------------------------------------------------------------------
-// LDS layouts (rows padded instead of swizzled, so every operand read is one
-// per-lane base plus a compile-time offset and both reads and staging writes
-// are bank-conflict free).  A tile holds the BNI = 64*SUB keys of one
-// iteration:
-//  K8 tile  [BNI keys][D] int8, row pitch D + 16 bytes
-//  V^T tile [D][BNI keys] 16-bit, row pitch 2*BNI + 8 bytes
-// ---------------------------------------------------------------------------
 __device__ __forceinline__ int remap_xcd(int w, int n) {
   const int per = n >> 3, rem = n & 7;
   const int xcd = w & 7, loc = w >> 3;
   return xcd * per + min(xcd, rem) + loc;
 }
 
-// max over the lanes {l, l^16, l^32, l^48} (the four lane groups holding one
-// q column of the score tile) with the gfx950 permlane swaps
-__device__ __forceinline__ int max_over_groups(int v) {
+// value of the partner lane l ^ 32 (the other half of a 32x32 C column)
+__device__ __forceinline__ int max_halves(int v) {
   const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  v = max((int)a[0], (int)a[1]);
-  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
-  return max((int)b[0], (int)b[1]);
+  return max((int)a[0], (int)a[1]);
+}
+__device__ __forceinline__ float sum_halves(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float((int)a[0]) + __int_as_float((int)a[1]);
 }
 
-// The int32 MFMA accumulator starts at the bit pattern of 2^23 + 2^22, so
-// it reads as the float 12582912 + S, exact for |S| < 2^22 (|S| <= 127^2*D).
-constexpr int kMagicI = 0x4B400000;
-constexpr float kMagicF = 12582912.0f;
-// A row's running max is only moved when a block's max exceeds it by more
-// than kTau (log2 units); P values are then bounded by 2^kTau.
-constexpr float kTau = 8.0f;
+// 4x4 byte transpose: out[i] = byte i of a, b, c, d
+__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&o)[4]) {
+  const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
+  const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
+  const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
+  const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030602u);  // c2 d2 c3 d3
+  o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+  o[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+  o[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+  o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+}
 
-// NW waves of QW query rows each; SUB 64-key sub-blocks per iteration (one
-// barrier and one prefetch per iteration).  One work-group per CU: NW/4 waves
-// per SIMD, so the compiler may use the whole register file.
-template <int D, int NW, int QW, int SUB, typename TV, typename PV, typename TO>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4, NW / 4))) void attn_fwd_kernel(
+// LDS column of the 4-key group kg (keys 4kg..4kg+3) of a V^T tile, in units
+// of 4 keys.  Key 32t + 8i + 4h + r sits at S^T row i*8 + 4h + r of key tile t,
+// i.e. in register 4i + r of lane half h; lane half h reads its 32 keys
+// contiguously from column 32h + 16t + 4i + r.
+__device__ __forceinline__ int vcol4(int kg) { return 8 * (kg & 1) + 4 * (kg >> 3) + ((kg >> 1) & 3); }
+
+// V staging source per P.V mode: TV elements (converted) or e4m3 codes
+template <typename TV, int PVM>
+struct VStage {
+  Raw8<TV> r[4];  // 4 keys x 8 channels
+};
+template <typename TV>
+struct VStage<TV, SAGE_PV_FP8> {
+  uint4 r[4];  // 4 keys x 16 channels of e4m3 codes
+};
+
+// QT 32-row q tiles per wave: QT = 1 -> 8 waves (2 per SIMD), everything in
+// arch VGPRs; QT = 2 -> 4 waves (1 per SIMD), O in the accumulation registers.
+template <int D, int QT, typename TV, int PVM, typename TO>
+__global__ __launch_bounds__(512 / QT) __attribute__((amdgpu_waves_per_eu(2 / QT, 2 / QT))) void attn_fwd_kernel(
     AttnArgs a) {
-  constexpr int NT = NW * 64;
-  constexpr int BM = NW * QW;   // q rows per work-group
-  constexpr int BN = 64;        // keys per softmax block (one k scale)
-  constexpr int BNI = BN * SUB; // keys per iteration
-  constexpr int QT = QW / 16;   // q tiles per wave
-  constexpr int DH = D / 64;    // 64-wide slices of the QK contraction
-  constexpr int DT = D / 16;    // 16-row d tiles of O^T
-  constexpr int KT = BN / 16;   // 16-key tiles per block
-  constexpr int CPR = D / 16;   // 16-byte chunks per K8 row
-  constexpr int KP = D + 16;    // K8 row pitch in LDS
-  constexpr int VPI = 2 * BNI + 8;  // V^T row pitch in LDS
-  constexpr int KB = BNI * KP;      // bytes of a K8 tile
-  constexpr int VB = D * VPI;       // bytes of a V^T tile
-  constexpr int KCH = BNI * CPR;            // 16-byte K8 chunks per tile
-  constexpr int VMT = (BNI / 2) * (D / 8);  // 2-key x 8-d micro-tiles per V tile
-  static_assert(KCH % 64 == 0 && VMT % 64 == 0, "staging work must be whole waves");
+  constexpr int NW = 8 / QT;      // waves per work-group
+  constexpr int NT = 64 * NW;     // threads per work-group
+  constexpr int QW = 32 * QT;     // query rows per wave
+  constexpr bool kQReg = QT == 1; // Q8 operand kept in registers (else read from LDS)
+  constexpr bool kF8 = PVM == SAGE_PV_FP8;
+  using Pv = PvT<PVM>;
+  constexpr int KC = D / 32;          // 32-byte slices of the QK contraction
+  constexpr int DT = D / 32;          // 32-row d tiles of O^T
+  constexpr int PW = Pv::kPW;         // P dwords per lane per q tile
+  constexpr int KP = D + 16;          // K8 tile row pitch (bytes)
+  constexpr int VP = 64 * Pv::kEB + 16;  // V^T tile row pitch (bytes)
+  constexpr int KTB = kBN * KP;
+  constexpr int VTB = D * VP;
+  constexpr int KCPR = D / 16;        // 16-byte chunks per K8 row
+  constexpr int KCH = kBN * KCPR;     // 16-byte chunks per K8 tile
   constexpr int KCH_T = (KCH + NT - 1) / NT;
-  constexpr int VMT_T = (VMT + NT - 1) / NT;
-  using Ops = PvOps<PV>;
+  constexpr int VCW = kF8 ? 16 : 8;   // channels per V micro-tile (4 keys each)
+  constexpr int VMT = (kBN / 4) * (D / VCW);  // V micro-tiles per tile
+  static_assert(KCH % NT == 0 || KCH < NT, "K staging");
+  static_assert(VMT <= NT, "V staging: one micro-tile per thread");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * KB + 2 * VB];
-  __shared__ float ksc_s[2][SUB];  // k scales of the tile in each buffer
-  char* const kbuf0 = smem;
-  char* const vbuf0 = smem + 2 * KB;
+  constexpr int QTB = kQReg ? 0 : kBM * KP;  // bytes of the work-group's Q8 rows in LDS
+  __shared__ __attribute__((aligned(16))) char smem[QTB + kKBuf * KTB + kVBuf * VTB];
+  __shared__ float ksc_s[kKBuf];
+  char* const qbuf = smem;
+  char* const kbuf0 = smem + QTB;
+  char* const vbuf0 = smem + QTB + kKBuf * KTB;
 
-  const int nqb = (a.Nq + BM - 1) / BM;
+  const int nqb = (a.Nq + kBM - 1) / kBM;
   const int wg = remap_xcd((int)blockIdx.x, (int)gridDim.x);
   int qb = wg % nqb;
   const int h = (wg / nqb) % a.Hq;
@@ -168,333 +239,399 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4,
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int g = lane >> 4, n = lane & 15;
-  const int q0 = qb * BM;
+  const int hh = lane >> 5, n = lane & 31;
+  const int q0 = qb * kBM;
   const int qa = q0 + wave * QW;  // first q row of this wave
 
   const int8_t* qbase = a.q8 + b * a.sq[0] + h * a.sq[1];
   const int8_t* kbase = a.k8 + b * a.sk[0] + hk * a.sk[1];
-  const TV* vbase = static_cast<const TV*>(a.v) + b * a.sv[0] + hk * a.sv[1];
   const float* ksc_base = a.k_scale + ((int64_t)b * a.Hkv + hk) * a.nks;
 
-  // ---- Q (B operand of S^T = K Q^T): q = qa + 16s + n, d = 64hh + 16g .. +16.
-  // Rows past Nq read the last row; their results are never stored.
-  v4i qreg[QT][DH];
+  // ---- Q8 (B operand of S^T = K Q^T): rows qa + 32s + n, bytes 32c + 16hh.
+  // Held in registers (QT = 1) or staged in LDS for the work-group (row pitch
+  // KP).  Rows past Nq read the last row; their results are never stored.
+  v4i qreg[QT][KC];
+  if constexpr (kQReg) {
+#pragma unroll
+    for (int s = 0; s < QT; ++s) {
+      const int row = min(qa + 32 * s + n, a.Nq - 1);
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+        qreg[s][c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 32 * c + 16 * hh));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < (kBM * KCPR) / NT; ++i) {
+      const int L = tid + i * NT;
+      const int row = min(q0 + L / KCPR, a.Nq - 1);
+      *reinterpret_cast<v4i*>(qbuf + (L / KCPR) * KP + 16 * (L % KCPR)) =
+          *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 16 * (L % KCPR)));
+    }
+  }
   float qsc[QT];
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    const int row = min(qa + 16 * s + n, a.Nq - 1);
-#pragma unroll
-    for (int hh = 0; hh < DH; ++hh)
-      qreg[s][hh] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 64 * hh + 16 * g));
-    const int si = min((qa + 16 * s) / a.q_sub, a.nqs - 1);
+    const int si = min((qa + 32 * s) / a.q_sub, a.nqs - 1);
     qsc[s] = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + si];
   }
 
-  // ---- key range (in 64-key blocks) of the work-group and of this wave
-  const int nkb_all = (a.Nkv + BN - 1) / BN;
+  // ---- key blocks of the work-group and of this wave
+  const int nkb_all = (a.Nkv + kBN - 1) / kBN;
   int nkb = nkb_all;
-  if (a.causal) nkb = min(nkb_all, (min(q0 + BM, a.Nq) - 1) / BN + 1);
-  const int nit = (nkb + SUB - 1) / SUB;      // iterations
+  if (a.causal) nkb = min(nkb_all, (min(q0 + kBM, a.Nq) - 1) / kBN + 1);
   const int q_last = min(qa + QW, a.Nq) - 1;  // last valid row of this wave (< qa if none)
-  int jmax = nkb - 1;                          // last 64-key block this wave needs
+  int jmax = nkb - 1;                           // last block this wave computes
   if (q_last < qa) jmax = -1;
-  else if (a.causal) jmax = min(jmax, q_last / BN);
+  else if (a.causal) jmax = min(jmax, q_last / kBN);
+  // leading blocks that need no mask: whole 64 keys inside Nkv and, when
+  // causal, every key <= the wave's first row
+  int nfull = a.Nkv / kBN;
+  if (a.causal) nfull = min(nfull, qa / kBN);
+  nfull = min(nfull, jmax + 1);
 
-  // ---- per-lane LDS read bases; tiles and halves are immediate offsets
-  const int kread = n * KP + 16 * g;   // + (64*sb + 16*t)*KP + 64*hh
-  const int vread = n * VPI + 8 * g;   // + dt*16*VPI + 2*(64*sb + 32*u + 16*hf)
-
-  // ---- staging.  K8: chunk L = tid + i*NT -> row L/CPR, column L%CPR.
-  // V: micro-tile m = tid + i*NT -> keys 2*(m%(BNI/2)) + {0,1}, d = 8*(m/(BNI/2)) .. +8.
+  // ---- staging: K8 chunk L = tid + i*256 -> row L / KCPR, chunk L % KCPR;
+  // V micro-tile m = tid -> keys 4*(m % 16) .. +4, channels VCW*(m / 16) .. +VCW.
   // Keys past Nkv read the last key: their P is 0 and the data is finite.
   v4i kst[KCH_T];
-  Raw8<TV> vst[VMT_T][2];
-  float kscst = 0.0f;  // lanes 0..SUB-1 of wave 0: the tile's k scales
-  auto load_tile = [&](int it) {
-    const int k0 = it * BNI;
-    if (wave == 0 && lane < SUB) kscst = ksc_base[min((it * SUB + lane) >> a.blkk_shift, a.nks - 1)];
+  VStage<TV, PVM> vst;
+  float kscst = 0.0f;
+  const int vkg = tid & 15, vcg = tid >> 4;
+  auto load_tile = [&](int j) __attribute__((always_inline)) {
+    const int k0 = j * kBN;
+    if (tid == 0) kscst = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int i = 0; i < KCH_T; ++i) {
-      if (wave * 64 + i * NT < KCH) {
-        const int L = tid + i * NT;
-        const int row = min(k0 + L / CPR, a.Nkv - 1);
-        kst[i] = *reinterpret_cast<const v4i*>(kbase + (uint32_t)(row * a.skn + 16 * (L % CPR)));
+      const int L = tid + i * NT;
+      if (KCH % NT == 0 || L < KCH) {
+        const int row = min(k0 + L / KCPR, a.Nkv - 1);
+        kst[i] = *reinterpret_cast<const v4i*>(kbase + (uint32_t)(row * a.skn + 16 * (L % KCPR)));
       }
     }
+    if (VMT == NT || tid < VMT) {
+      if constexpr (kF8) {
+        const uint8_t* vb = static_cast<const uint8_t*>(a.v) + b * a.sv[0] + hk * a.sv[1];
 #pragma unroll
-    for (int i = 0; i < VMT_T; ++i) {
-      if (wave * 64 + i * NT < VMT) {
-        const int m = tid + i * NT;
-        const int key = k0 + 2 * (m % (BNI / 2));
-        const int col = 8 * (m / (BNI / 2));
-        vst[i][0] = load8<TV>(vbase + (uint32_t)(min(key, a.Nkv - 1) * a.svn + col));
-        vst[i][1] = load8<TV>(vbase + (uint32_t)(min(key + 1, a.Nkv - 1) * a.svn + col));
+        for (int r = 0; r < 4; ++r)
+          vst.r[r] = *reinterpret_cast<const uint4*>(vb + (uint32_t)(min(k0 + 4 * vkg + r, a.Nkv - 1) * a.svn +
+                                                                      VCW * vcg));
+      } else {
+        const TV* vb = static_cast<const TV*>(a.v) + b * a.sv[0] + hk * a.sv[1];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          vst.r[r] = load8<TV>(vb + (uint32_t)(min(k0 + 4 * vkg + r, a.Nkv - 1) * a.svn + VCW * vcg));
       }
     }
   };
-  auto store_tile = [&](int buf) {
-    char* ks = kbuf0 + buf * KB;
-    char* vs = vbuf0 + buf * VB;
-    if (wave == 0 && lane < SUB) ksc_s[buf][lane] = kscst;
+  auto store_tile = [&](int j) __attribute__((always_inline)) {
+    char* ks = kbuf0 + (j & 1) * KTB;
+    char* vs = vbuf0 + (j & 3) * VTB;
+    if (tid == 0) ksc_s[j & 1] = kscst;
 #pragma unroll
     for (int i = 0; i < KCH_T; ++i) {
-      if (wave * 64 + i * NT < KCH) {
-        const int L = tid + i * NT;
-        *reinterpret_cast<v4i*>(ks + (L / CPR) * KP + 16 * (L % CPR)) = kst[i];
-      }
+      const int L = tid + i * NT;
+      if (KCH % NT == 0 || L < KCH)
+        *reinterpret_cast<v4i*>(ks + (L / KCPR) * KP + 16 * (L % KCPR)) = kst[i];
     }
+    if (VMT == NT || tid < VMT) {
+      char* dst = vs + VCW * vcg * VP + 4 * Pv::kEB * vcol4(vkg);
+      if constexpr (kF8) {
 #pragma unroll
-    for (int i = 0; i < VMT_T; ++i) {
-      if (wave * 64 + i * NT < VMT) {
-        const int m = tid + i * NT;
-        char* dst = vs + 8 * (m / (BNI / 2)) * VPI + 4 * (m % (BNI / 2));
+        for (int w = 0; w < 4; ++w) {
+          uint32_t t[4];
+          transpose4x4(word(vst.r[0], w), word(vst.r[1], w), word(vst.r[2], w), word(vst.r[3], w), t);
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          *reinterpret_cast<uint32_t*>(dst + e * VPI) = Ops::pack2(elem<TV>(vst[i][0], e), elem<TV>(vst[i][1], e));
+          for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(dst + (4 * w + e) * VP) = t[e];
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v2i w = {(int)Pv::pack2(elem<TV>(vst.r[0], e), elem<TV>(vst.r[1], e)),
+                   (int)Pv::pack2(elem<TV>(vst.r[2], e), elem<TV>(vst.r[3], e))};
+          *reinterpret_cast<v2i*>(dst + e * VP) = w;
+        }
       }
     }
   };
 
-  // ---- accumulators
-  v4f oacc[DT][QT];
-  v4f lacc[QT];  // row sums of P via MFMA with an all-ones A operand
+  // ---- accumulators and softmax state
+  v16f oacc[DT][QT];
+  float m_use[QT], lsum[QT], alpha_o[QT];  // lsum: this lane's share of the row sums
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    lacc[s] = (v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[dt][s] = (v4f){0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt < DT; ++dt) oacc[dt][s] = (v16f){};
+    m_use[s] = -INFINITY;
+    lsum[s] = 0.0f;
+    alpha_o[s] = 1.0f;
   }
-  float m_use[QT];
-#pragma unroll
-  for (int s = 0; s < QT; ++s) m_use[s] = -INFINITY;
-  const v4i ones = Ops::ones();
+  bool pend = false;  // O must be multiplied by alpha_o before the next P.V
+  v16i S[2][QT];      // S^T of key tile t, q tile s
+  float ksc_cur = 0.0f;           // k scale of the block held in S
+  uint32_t Pprev[QT][PW], Pcur[QT][PW];  // P of blocks j-1 and j
+  const v16i magic = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
+                      kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
 
-  // ---- building blocks.  Operand reads are separate from the MFMAs that
-  // use them so a phase can issue its reads first; the generic path fences
-  // reads from MFMAs with a scheduling barrier, the hot path interleaves them
-  // explicitly (see below).
-  // K8 operand (t, hh) of sub-block sb: rows 16t + n, bytes 64hh + 16g .. +16
-  auto read_k = [&](int buf, int sb, v4i (&ka)[KT][DH]) {
-    const char* ks = kbuf0 + buf * KB + kread + sb * 64 * KP;
+  // ---- building blocks
+  // S^T of block j (its K8 tile in buffer j & 1)
+  // Q operand (s, c): row 32s + n of the wave's rows, bytes 32c + 16hh .. +16
+  const char* qrd = qbuf + (wave * QW + n) * KP + 16 * hh;
+  auto qk = [&](int j) __attribute__((always_inline)) {
+    const char* ks = kbuf0 + (j & 1) * KTB + n * KP + 16 * hh;
+    ksc_cur = ksc_s[j & 1];
+    v4i qb[QT][KC];
 #pragma unroll
-    for (int t = 0; t < KT; ++t)
+    for (int s = 0; s < QT; ++s)
 #pragma unroll
-      for (int hh = 0; hh < DH; ++hh) ka[t][hh] = *reinterpret_cast<const v4i*>(ks + t * 16 * KP + 64 * hh);
-  };
-  auto mma_qk = [&](const v4i (&ka)[KT][DH], v4i (&sacc)[KT][QT]) {
+      for (int c = 0; c < KC; ++c)
+        qb[s][c] = kQReg ? qreg[s][c] : *reinterpret_cast<const v4i*>(qrd + 32 * s * KP + 32 * c);
 #pragma unroll
-    for (int t = 0; t < KT; ++t) {
+    for (int t = 0; t < 2; ++t) {
+      v4i ka[KC];
 #pragma unroll
-      for (int s = 0; s < QT; ++s) sacc[t][s] = (v4i){kMagicI, kMagicI, kMagicI, kMagicI};
+      for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const v4i*>(ks + 32 * t * KP + 32 * c);
 #pragma unroll
-      for (int hh = 0; hh < DH; ++hh)
+      for (int c = 0; c < KC; ++c)
 #pragma unroll
         for (int s = 0; s < QT; ++s)
-          sacc[t][s] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka[t][hh], qreg[s][hh], sacc[t][s], 0, 0, 0);
+          S[t][s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qb[s][c], c == 0 ? magic : S[t][s], 0, 0, 0);
     }
   };
-  // V^T operand (dt) of half u of sub-block sb: rows 16dt + n, keys
-  // 32u + 4g..+3 and 32u + 16 + 4g..+3 of the sub-block
-  auto read_v = [&](int buf, int sb, int u, v4i (&va)[DT]) {
-    const char* vs = vbuf0 + buf * VB + vread + sb * 128 + 64 * u;
+  // O^T += V^T P^T of block j (its V^T tile in buffer j & 3)
+  auto pv = [&](int j, const uint32_t (&P)[QT][PW]) __attribute__((always_inline)) {
+    const char* vs = vbuf0 + (j & 3) * VTB + n * VP;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const v2i lo = *reinterpret_cast<const v2i*>(vs + dt * 16 * VPI);
-      const v2i hi = *reinterpret_cast<const v2i*>(vs + dt * 16 * VPI + 32);
-      va[dt] = (v4i){lo.x, lo.y, hi.x, hi.y};
+      const char* vr = vs + 32 * dt * VP;
+      if constexpr (kF8) {
+        const v4i lo = *reinterpret_cast<const v4i*>(vr + 32 * hh);
+        const v4i hi = *reinterpret_cast<const v4i*>(vr + 32 * hh + 16);
+        const v8i va = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+        for (int s = 0; s < QT; ++s) {
+          const v8i pb = {(int)P[s][0], (int)P[s][1], (int)P[s][2], (int)P[s][3],
+                          (int)P[s][4], (int)P[s][5], (int)P[s][6], (int)P[s][7]};
+          oacc[dt][s] = Pv::mma(va, pb, oacc[dt][s]);
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {  // 16-key steps: key tile kk/2, register half kk%2
+          const v4i va = *reinterpret_cast<const v4i*>(vr + 64 * hh + 16 * kk);
+#pragma unroll
+          for (int s = 0; s < QT; ++s) {
+            const v4i pb = {(int)P[s][4 * kk], (int)P[s][4 * kk + 1], (int)P[s][4 * kk + 2], (int)P[s][4 * kk + 3]};
+            oacc[dt][s] = Pv::mma(va, pb, oacc[dt][s]);
+          }
+        }
+      }
     }
   };
-  auto mma_pv = [&](const v4i (&va)[DT], int u, const v4i (&pk)[QT][2]) {
-#pragma unroll
-    for (int s = 0; s < QT; ++s) lacc[s] = Ops::mfma(ones, pk[s][u], lacc[s]);
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int s = 0; s < QT; ++s) oacc[dt][s] = Ops::mfma(va[dt], pk[s][u], oacc[dt][s]);
+  // key of register v of key tile t in this lane, relative to the block
+  auto key_of = [&](int t, int v) __attribute__((always_inline)) {
+    return 32 * t + 8 * (v >> 2) + 4 * hh + (v & 3);
   };
-  auto qk = [&](int buf, int sb, v4i (&sacc)[KT][QT]) {
-    v4i ka[KT][DH];
-    read_k(buf, sb, ka);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_qk(ka, sacc);
+  auto key_ok = [&](int key, int qrow) __attribute__((always_inline)) {
+    return key < a.Nkv && (!a.causal || key <= qrow);
   };
-  auto pv = [&](int buf, int sb, const v4i (&pk)[QT][2]) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      v4i va[DT];
-      read_v(buf, sb, u, va);
-      __builtin_amdgcn_sched_barrier(0);
-      mma_pv(va, u, pk);
-    }
-  };
-  auto key_ok = [&](int key, int qrow) { return key < a.Nkv && (!a.causal || key <= qrow); };
-  // block max of each q column of 64-key block kb (log2 units; -inf if all masked)
-  auto rowmax = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], float (&mblk)[QT], bool masked) {
-    const int k0 = kb * BN;
+  // softmax of block j held in S -> P (and the running max / sums)
+  auto softmax = [&](int j, uint32_t (&P)[QT][PW], bool masked) __attribute__((always_inline)) {
+    const int k0 = j * kBN;
 #pragma unroll
     for (int s = 0; s < QT; ++s) {
-      const int qrow = qa + 16 * s + n;
+      const int qrow = qa + 32 * s + n;
+      const float c = qsc[s] * ksc_cur;
       int mx = INT_MIN;
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          int v = sacc[t][s][r];
-          if (masked) v = key_ok(k0 + 16 * t + 4 * g + r, qrow) ? v : INT_MIN;
-          mx = max(mx, v);
+        for (int v = 0; v < 16; ++v) {
+          int x = S[t][s][v];
+          if (masked) x = key_ok(k0 + key_of(t, v), qrow) ? x : INT_MIN;
+          mx = max(mx, x);
         }
-      mx = max_over_groups(mx);
-      mblk[s] = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * (qsc[s] * ksc);
-    }
-  };
-  // lazy max update: returns whether O and the row sums must be rescaled by
-  // alpha[] (wave-uniform; applied by the caller at the right point)
-  auto decide = [&](const float (&mblk)[QT], float (&alpha)[QT]) -> bool {
-    bool need = false;
-#pragma unroll
-    for (int s = 0; s < QT; ++s) need |= mblk[s] > m_use[s] + kTau;
-    const bool rescale = __builtin_amdgcn_ballot_w64(need) != 0;
-#pragma unroll
-    for (int s = 0; s < QT; ++s) alpha[s] = 1.0f;
-    if (rescale) {
-#pragma unroll
-      for (int s = 0; s < QT; ++s) {
-        const float mn = fmaxf(m_use[s], mblk[s]);
-        alpha[s] = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_use[s] - mn);
-        m_use[s] = mn;
-      }
-    }
-    return rescale;
-  };
-  // P = exp2(S*c - m) of q tile s in B-operand layout (16-bit pairs)
-  auto exps_s = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2], int s, bool masked) {
-    const int k0 = kb * BN;
-    {
-      const float c = qsc[s] * ksc;
-      const float m = m_use[s] == -INFINITY ? 0.0f : m_use[s];
+      mx = max_halves(mx);
+      const float mblk = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * c;
+      // lazy max update (per q column; both lane halves agree)
+      const bool need = mblk > m_use[s] + SoftmaxCfg<PVM>::kTau;
+      const float mnew = need ? mblk : m_use[s];
+      const float alpha = need ? __builtin_amdgcn_exp2f(m_use[s] - mnew) : 1.0f;
+      m_use[s] = mnew;
+      lsum[s] *= alpha;
+      alpha_o[s] *= alpha;
+      pend |= __builtin_amdgcn_ballot_w64(need) != 0;
+      const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
       const float bias = __builtin_fmaf(kMagicF, c, m);  // x = (2^23+2^22+S)*c - bias = S*c - m
-      const int qrow = qa + 16 * s + n;
-      float p[KT][4];
+      float ls = 0.0f;
 #pragma unroll
-      for (int t = 0; t < KT; ++t)
+      for (int t = 0; t < 2; ++t) {
+        float p[16];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float x = __builtin_fmaf(__int_as_float(sacc[t][s][r]), c, -bias);
-          float e = __builtin_amdgcn_exp2f(x);
-          if (masked) e = key_ok(k0 + 16 * t + 4 * g + r, qrow) ? e : 0.0f;
-          p[t][r] = e;
+        for (int v = 0; v < 16; ++v) {
+          float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(S[t][s][v]), c, -bias));
+          if (masked) e = key_ok(k0 + key_of(t, v), qrow) ? e : 0.0f;
+          p[v] = e;
+          ls += e;
         }
+        if constexpr (kF8) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        pk[s][u].x = (int)Ops::pack2(p[2 * u][0], p[2 * u][1]);
-        pk[s][u].y = (int)Ops::pack2(p[2 * u][2], p[2 * u][3]);
-        pk[s][u].z = (int)Ops::pack2(p[2 * u + 1][0], p[2 * u + 1][1]);
-        pk[s][u].w = (int)Ops::pack2(p[2 * u + 1][2], p[2 * u + 1][3]);
+          for (int w = 0; w < 4; ++w) P[s][4 * t + w] = Pv::pack4(p[4 * w], p[4 * w + 1], p[4 * w + 2], p[4 * w + 3]);
+        } else {
+#pragma unroll
+          for (int w = 0; w < 8; ++w) P[s][8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
+        }
+      }
+      lsum[s] += ls;
+    }
+  };
+  // scheduling pattern of the fast path: per d tile, its V^T reads, then
+  // each P.V MFMA followed by a share of the softmax VALU work
+  auto interleave = [&]() __attribute__((always_inline)) {
+    constexpr int kMma = kF8 ? QT : 4 * QT;  // MFMAs per d tile
+    constexpr int kRd = kF8 ? 2 : 4;         // ds_read_b128 per d tile
+    constexpr int kValu = (150 * QT + DT * kMma - 1) / (DT * kMma);  // softmax VALU share per MFMA
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      __builtin_amdgcn_sched_group_barrier(0x100, kRd, 0);
+#pragma unroll
+      for (int m = 0; m < kMma; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
       }
     }
   };
-  auto exps = [&](int kb, float ksc, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2], bool masked) {
-#pragma unroll
-    for (int s = 0; s < QT; ++s) exps_s(kb, ksc, sacc, pk, s, masked);
-  };
-  auto apply_rescale = [&](const float (&alpha)[QT]) {
+  auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < QT; ++s) {
-      lacc[s] *= alpha[s];
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha[s];
+      for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha_o[s];
+      alpha_o[s] = 1.0f;
     }
   };
-  auto is_masked = [&](int kb) {
-    const int k0 = kb * BN;
-    return (k0 + BN > a.Nkv) || (a.causal && k0 + BN - 1 > qa);
+
+  // ---- one iteration: P.V of block j-1, softmax of block j, S of block j+1,
+  // staging of tile j+2.  Iteration nkb only finishes the last P.V.
+  // ---- iterations.  Iteration j: P.V of block j-1, softmax of block j, S of
+  // block j+1, staging of tile j+2; iteration nkb only finishes the last P.V.
+  // Every wave runs nkb + 1 iterations (one barrier each).  The mask-free
+  // steady state has a loop of its own so that the O accumulators are
+  // updated from one place in each loop.
+  auto keep_p = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < QT; ++s)
+#pragma unroll
+      for (int w = 0; w < PW; ++w) Pprev[s][w] = Pcur[s][w];
   };
-  // generic order for one 64-key block (masked blocks, partially active tiles)
-  auto block_generic = [&](int buf, int sb, int kb, const v4i (&sacc)[KT][QT], v4i (&pk)[QT][2]) {
-    const float ksc = ksc_s[buf][sb];
-    const bool masked = is_masked(kb);
-    float mblk[QT], alpha[QT];
-    if (masked) rowmax(kb, ksc, sacc, mblk, true);
-    else rowmax(kb, ksc, sacc, mblk, false);
-    if (decide(mblk, alpha)) apply_rescale(alpha);
-    if (masked) exps(kb, ksc, sacc, pk, true);
-    else exps(kb, ksc, sacc, pk, false);
-    pv(buf, sb, pk);
+  auto finish = [&](int j, bool stage) __attribute__((always_inline)) {
+    if (j + 1 <= jmax) qk(j + 1);
+    if (stage) store_tile(j + 2);
+    __syncthreads();
+  };
+  auto generic_iter = [&](int j) __attribute__((always_inline)) {
+    const bool stage = j + 2 < nkb;
+    if (stage) load_tile(j + 2);
+    if (pend) {
+      rescale_o();
+      pend = false;
+    }
+    if (j >= 1 && j - 1 <= jmax) pv(j - 1, Pprev);
+    __builtin_amdgcn_sched_barrier(0);
+    if (j <= jmax) {
+      if (j < nfull) softmax(j, Pcur, false);
+      else softmax(j, Pcur, true);
+      keep_p();
+    }
+    finish(j, stage);
+  };
+  // blocks 1 <= j < j_fast: P.V of block j-1 (MFMA) interleaved with the
+  // softmax of block j (VALU); S of block j+1 and tile j+2 always exist.
+  // The empty asm statements pin values where the pipeline needs them: P
+  // computed before the QK MFMAs, S written to arch registers, O in the
+  // accumulation registers across iterations.
+  auto fast_iter = [&](int j) __attribute__((always_inline)) {
+    load_tile(j + 2);
+    if (pend) {
+      rescale_o();
+      pend = false;
+    }
+    pv(j - 1, Pprev);
+    softmax(j, Pcur, false);
+    interleave();
+#pragma unroll
+    for (int s = 0; s < QT; ++s)
+#pragma unroll
+      for (int w = 0; w < PW; ++w) asm volatile("" ::"v"(Pcur[s][w]));
+    keep_p();
+    qk(j + 1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int s = 0; s < QT; ++s) asm volatile("" : "+v"(S[t][s]));
+    store_tile(j + 2);
+    if constexpr (QT == 2) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int s = 0; s < QT; ++s) asm volatile("" : "+a"(oacc[dt][s]));
+    }
+    __syncthreads();
   };
 
-  // ---- main loop: iteration it stages tile it+1 (global loads in flight
-  // during the compute) and computes the SUB 64-key blocks of tile it.  The
-  // QK of every sub-block is issued before the first softmax.
+  // ---- prologue: tiles 0 and 1 staged, S of block 0
   load_tile(0);
   store_tile(0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int it = 0; it < nit; ++it) {
-    const bool more = it + 1 < nit;
-    if (more) load_tile(it + 1);
-    const int buf = it & 1;
-    const int kb0 = it * SUB;
-    if (kb0 <= jmax) {
-      v4i S[SUB][KT][QT];
-      v4i P[QT][2];
-#pragma unroll
-      for (int sb = 0; sb < SUB; ++sb)
-        if (kb0 + sb <= jmax) qk(buf, sb, S[sb]);
-#pragma unroll
-      for (int sb = 0; sb < SUB; ++sb)
-        if (kb0 + sb <= jmax) block_generic(buf, sb, kb0 + sb, S[sb], P);
-    }
-    if (more) store_tile((it + 1) & 1);
-    __syncthreads();
+  if (nkb > 1) {
+    load_tile(1);
+    store_tile(1);
   }
+  __syncthreads();
+  if (jmax >= 0) qk(0);
+  __syncthreads();  // block 0's K8 buffer is restaged in iteration 0
 
-  // ---- epilogue: O / l, store rows q = qa + 16s + n, d = 16dt + 4g .. +4
+  const int j_fast = min(min(nfull, jmax), nkb - 2);
+  generic_iter(0);
+  int j = 1;
+  for (; j < j_fast; ++j) fast_iter(j);
+  for (; j <= nkb; ++j) generic_iter(j);
+
+  // ---- epilogue: O / l, store rows q = qa + 32s + n, d = 32dt + 8i + 4hh .. +4
+  if (pend) rescale_o();
   TO* obase = static_cast<TO*>(a.o) + b * a.so[0] + h * a.so[1];
+  const float* vsc = kF8 ? a.v_scale + ((int64_t)b * a.Hkv + hk) * D : nullptr;
 #pragma unroll
   for (int s = 0; s < QT; ++s) {
-    const float inv = 1.0f / lacc[s][0];
-    const int row = qa + 16 * s + n;
+    const float inv = 1.0f / sum_halves(lsum[s]);
+    const int row = qa + 32 * s + n;
     if (row < a.Nq) {
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const v4f o = oacc[dt][s] * inv;
-        store4<TO>(obase + (uint32_t)(row * a.son + 16 * dt + 4 * g), o.x, o.y, o.z, o.w);
-      }
+      for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d0 = 32 * dt + 8 * i + 4 * hh;
+          float4 f = make_float4(inv, inv, inv, inv);
+          if constexpr (kF8) {
+            const float4 vs4 = *reinterpret_cast<const float4*>(vsc + d0);
+            f = make_float4(inv * vs4.x, inv * vs4.y, inv * vs4.z, inv * vs4.w);
+          }
+          const v16f& o = oacc[dt][s];
+          store4<TO>(obase + (uint32_t)(row * a.son + d0), o[4 * i] * f.x, o[4 * i + 1] * f.y, o[4 * i + 2] * f.z,
+                     o[4 * i + 3] * f.w);
+        }
     }
   }
 }
 
-template <int D, int NW, int QW, int SUB, typename TV, typename PV>
+template <int D, typename TV, int PVM, typename TO>
 static int launch_cfg(const AttnArgs& a, hipStream_t st) {
-  constexpr int BM = NW * QW;
-  const int64_t nqb = (a.Nq + BM - 1) / BM;
+  constexpr int QT = 1;
+  const int64_t nqb = (a.Nq + kBM - 1) / kBM;
   const int64_t grid = nqb * a.Hq * a.B;
   if (grid > 0x7FFFFFFF) return fail("sage_attn_fwd: invalid argument: grid too large");
-  hipLaunchKernelGGL((attn_fwd_kernel<D, NW, QW, SUB, TV, PV, TV>), dim3((unsigned)grid), dim3(NW * 64), 0, st,
-                     a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, QT, TV, PVM, TO>), dim3((unsigned)grid), dim3(512 / QT), 0, st, a);
   return check_launch("sage_attn_fwd");
 }
 
-// Tiling variant: 0 = 8 waves x 32 rows, 64 keys per iteration (default);
-// 1 = 8 waves x 32 rows, 128 keys per iteration.  SAGE_ATTN_VARIANT selects.
-static int attn_variant() {
-  static int v = [] {
-    const char* e = getenv("SAGE_ATTN_VARIANT");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
-template <int D, typename TV, typename PV>
-static int launch_attn(const AttnArgs& a, hipStream_t st) {
-  if (attn_variant() == 1) return launch_cfg<D, 8, 32, 2, TV, PV>(a, st);
-  return launch_cfg<D, 8, 32, 1, TV, PV>(a, st);
-}
-
-template <typename TV, typename PV>
-static int launch_attn_d(const AttnArgs& a, int D, hipStream_t st) {
-  return D == 64 ? launch_attn<64, TV, PV>(a, st) : launch_attn<128, TV, PV>(a, st);
+template <typename TV, int PVM, typename TO>
+static int launch_d(const AttnArgs& a, int D, hipStream_t st) {
+  return D == 64 ? launch_cfg<64, TV, PVM, TO>(a, st) : launch_cfg<128, TV, PVM, TO>(a, st);
 }
 
 static bool strides_ok(const int64_t* s, int esize) {
@@ -502,6 +639,8 @@ static bool strides_ok(const int64_t* s, int esize) {
     if (s[i] < 0 || (s[i] * esize) % 16 != 0) return false;
   return true;
 }
+
+static bool is_float_code(int c) { return c == SAGE_DTYPE_F32 || c == SAGE_DTYPE_F16 || c == SAGE_DTYPE_BF16; }
 
 }  // namespace sage
 
@@ -522,20 +661,27 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
     return fail("sage_attn_fwd: invalid argument: shape too large");
   if (blkk != 64 && blkk != 128 && blkk != 256)
     return fail("sage_attn_fwd: invalid argument: blkk=%d (64, 128 or 256)", blkk);
-  if (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0)
-    return fail("sage_attn_fwd: invalid argument: q_sub=%d blkq=%d", q_sub, blkq);
+  if (q_sub < 32 || q_sub % 32 != 0 || blkq % q_sub != 0)
+    return fail("sage_attn_fwd: invalid argument: q_sub=%d blkq=%d (q_sub: a multiple of 32 dividing blkq)", q_sub,
+                blkq);
   if (!q8 || !q_scale || !k8 || !k_scale || !v || !o || !q8_strides || !k8_strides || !v_strides || !o_strides)
     return fail("sage_attn_fwd: invalid argument: null pointer");
-  if (v_dtype != o_dtype || (v_dtype != SAGE_DTYPE_F32 && v_dtype != SAGE_DTYPE_F16 && v_dtype != SAGE_DTYPE_BF16))
+  if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16 && pv_mode != SAGE_PV_FP8)
+    return fail("sage_attn_fwd: invalid argument: pv_mode %d", pv_mode);
+  if (!is_float_code(o_dtype)) return fail("sage_attn_fwd: invalid argument: o_dtype %d", o_dtype);
+  if (pv_mode == SAGE_PV_FP8) {
+    if (v_dtype != SAGE_DTYPE_FP8E4M3 || !v_scale)
+      return fail("sage_attn_fwd: invalid argument: FP8 P.V needs e4m3 V codes and v_scale");
+  } else if (v_dtype != o_dtype) {
     return fail("sage_attn_fwd: invalid argument: v_dtype %d / o_dtype %d", v_dtype, o_dtype);
-  if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16)
-    return fail("sage_attn_fwd: invalid argument: pv_mode %d not available", pv_mode);
-  const int es = v_dtype == SAGE_DTYPE_F32 ? 4 : 2;
+  }
+  const int ves = v_dtype == SAGE_DTYPE_F32 ? 4 : (v_dtype == SAGE_DTYPE_FP8E4M3 ? 1 : 2);
+  const int oes = o_dtype == SAGE_DTYPE_F32 ? 4 : 2;
   const bool rows32 = Nq * q8_strides[2] + D < 0x7FFFFFFF && Nkv * k8_strides[2] + D < 0x7FFFFFFF &&
                       Nkv * v_strides[2] + D < 0x7FFFFFFF && Nq * o_strides[2] + D < 0x7FFFFFFF;
   if (!rows32) return fail("sage_attn_fwd: invalid argument: a head's rows must span < 2^31 elements");
-  if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(v_strides, es) ||
-      !strides_ok(o_strides, es))
+  if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(v_strides, ves) ||
+      !strides_ok(o_strides, oes))
     return fail("sage_attn_fwd: invalid argument: strides must keep 16-byte aligned rows");
   if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v | (uintptr_t)o) % 16 != 0)
     return fail("sage_attn_fwd: invalid argument: base pointers must be 16-byte aligned");
@@ -569,14 +715,22 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   a.nqs = (int)(((Nq + blkq - 1) / blkq) * (blkq / q_sub));
   a.nks = (int)((Nkv + blkk - 1) / blkk);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const int d = (int)D;
+  if (pv_mode == SAGE_PV_FP8) {
+    switch (o_dtype) {
+      case SAGE_DTYPE_F32: return launch_d<uint8_t, SAGE_PV_FP8, float>(a, d, st);
+      case SAGE_DTYPE_F16: return launch_d<uint8_t, SAGE_PV_FP8, _Float16>(a, d, st);
+      default: return launch_d<uint8_t, SAGE_PV_FP8, __bf16>(a, d, st);
+    }
+  }
   const bool bf = pv_mode == SAGE_PV_BF16;
   switch (v_dtype) {
     case SAGE_DTYPE_F32:
-      return bf ? launch_attn_d<float, __bf16>(a, (int)D, st) : launch_attn_d<float, _Float16>(a, (int)D, st);
+      return bf ? launch_d<float, SAGE_PV_BF16, float>(a, d, st) : launch_d<float, SAGE_PV_F16, float>(a, d, st);
     case SAGE_DTYPE_F16:
-      return bf ? launch_attn_d<_Float16, __bf16>(a, (int)D, st)
-                : launch_attn_d<_Float16, _Float16>(a, (int)D, st);
+      return bf ? launch_d<_Float16, SAGE_PV_BF16, _Float16>(a, d, st)
+                : launch_d<_Float16, SAGE_PV_F16, _Float16>(a, d, st);
     default:
-      return bf ? launch_attn_d<__bf16, __bf16>(a, (int)D, st) : launch_attn_d<__bf16, _Float16>(a, (int)D, st);
+      return bf ? launch_d<__bf16, SAGE_PV_BF16, __bf16>(a, d, st) : launch_d<__bf16, SAGE_PV_F16, __bf16>(a, d, st);
   }
 }
