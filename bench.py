@@ -145,7 +145,6 @@ def main(argv=None) -> int:
     causal = bool(inp["causal"])
     pv = case.get("pv_dtype", "fp16")
     q_sub = H.WAVE_ROWS if case.get("q_gran") == "wave" else 128
-    v_fp8 = pv == "fp8"
     B, Hq, N, D = q.shape
     est = R.estimate(case)
     metric_ops, algo_ops = float(est["flops"]), float(est["algo_flops"])
@@ -156,7 +155,7 @@ def main(argv=None) -> int:
     def step(ev=None):
         if ev is not None:
             ev[0].record(stream)
-        pre = H.prepass(q, k, v, q_sub=q_sub, smooth_k=True, v_fp8=v_fp8)
+        pre = H.prepass(q, k, v, q_sub=q_sub, smooth_k=True, pv_dtype=pv)
         if ev is not None:
             ev[1].record(stream)
         H.attention(q, k, v, pre, causal, pv_dtype=pv, q_sub=q_sub, out=out)
@@ -182,6 +181,7 @@ def main(argv=None) -> int:
     step_ms = np.array([e[0].elapsed_time(e[2]) for e in evs])
 
     value = metric_ops / (ms * 1e-3) / 1e12
+    pre_bytes = est["prepass_bytes"] + est["vtile_bytes"]  # quantization + V tiles
     achieved = algo_ops / (float(attn_ms.mean()) * 1e-3) / 1e12
     res = {
         "metric": "sage_attn effective TOPS (4*B*H*N^2*D/t)",
@@ -202,10 +202,9 @@ def main(argv=None) -> int:
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
         "latency_ms": {"p50": round(float(np.percentile(step_ms, 50)), 4),
                        "p95": round(float(np.percentile(step_ms, 95)), 4)},
-        "prepass": {"ms": round(float(pre_ms.mean()), 4),
-                    "gbps": round(est["prepass_bytes"] / (float(pre_ms.mean()) * 1e-3) / 1e9, 1),
-                    "hbm_frac": round(est["prepass_bytes"] / (float(pre_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-                                      4)},
+        "prepass": {"ms": round(float(pre_ms.mean()), 4), "bytes": pre_bytes,
+                    "gbps": round(pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9, 1),
+                    "hbm_frac": round(pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
         "roofline": {"kernel": "attn_fwd_kernel", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
                      "traffic": _traffic_from_profiles(args.config),

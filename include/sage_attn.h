@@ -8,6 +8,8 @@
  *                      quant_per_block_int8_kernel() triton_impl.py:7-33
  *                      (+ the K channel-mean hook     triton_impl.py:39-40,
  *                         + FP8 V, which the reference does not have)
+ *   sage_vtiles()   <- v.to(torch.float16)            triton_impl.py:189
+ *                      (fused with the attention's V tile layout)
  *   sage_attn_fwd() <- _attn_fwd[grid](...) launch    triton_impl.py:186-199
  *                      _attn_fwd / _attn_fwd_inner    triton_impl.py:86-160
  *
@@ -39,28 +41,34 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 1
+#define SAGE_ABI_VERSION 2
 
 /* element types (dtype codes used by every entry point) */
 #define SAGE_DTYPE_F32 0
 #define SAGE_DTYPE_F16 1
 #define SAGE_DTYPE_BF16 2
 #define SAGE_DTYPE_FP8E4M3 3 /* OCP e4m3 ("e4m3fn"), bias 7, max 448 */
+#define SAGE_DTYPE_VTILES 4  /* V in the tile layout of sage_vtiles() (type set by pv_mode) */
 
 /* v_mode of sage_prepass */
-#define SAGE_V_NONE 0 /* V is not touched by the pre-pass */
-#define SAGE_V_FP8 1  /* per-channel FP8 e4m3 V: v8 = RNE_sat(v / v_scale[c]) */
+#define SAGE_V_NONE 0      /* V is not touched by the pre-pass */
+#define SAGE_V_FP8 1       /* per-channel FP8 e4m3 V: v_scale[c] = max|v[:,c]| / 448 and
+                              v8 = RNE_sat(v / v_scale[c]), row-major like v */
+#define SAGE_V_FP8_SCALE 2 /* v_scale only (for sage_vtiles with SAGE_PV_FP8) */
 
 /* pv_mode of sage_attn_fwd: the operand type of the P.V product */
 #define SAGE_PV_F16 0  /* P and V rounded to fp16 (the reference's choice, triton_impl.py:112-113,189) */
 #define SAGE_PV_BF16 1 /* P and V in bf16 */
-#define SAGE_PV_FP8 2  /* P and V in FP8 e4m3; V comes from sage_prepass(v_mode=SAGE_V_FP8) */
+#define SAGE_PV_FP8 2  /* P and V in FP8 e4m3 with per-channel V scales */
 
 /* Library version; bumped whenever a signature below changes. */
 int sage_abi_version(void);
 
 /* Message of the last failed call on the calling thread ("" if none). */
 const char* sage_last_error(void);
+
+/* Bytes of the V tile buffer of sage_vtiles() for the given problem and pv_mode. */
+size_t sage_vtile_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t D, int pv_mode);
 
 /* Bytes of scratch that sage_prepass needs for the given problem
  * (the per-chunk K channel sums and V channel maxima). */
@@ -84,6 +92,7 @@ size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t
  *            k8 [B,Hkv,Nkv,D] int8 + k_scale [B,Hkv,ceil(Nkv/blkk)]
  *            km [B,Hkv,D] fp32 (written when smooth_k; may be NULL otherwise)
  *            v8 [B,Hkv,Nkv,D] e4m3 bytes + v_scale [B,Hkv,D] (v_mode FP8)
+ *            v_scale only (v_mode FP8_SCALE; v8 may be NULL)
  *  q8/k8/v8 strides are given like the input strides; scales, km and
  *  v_scale are dense.
  */
@@ -96,12 +105,32 @@ int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int6
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * V converted to the P.V operand type and laid out in tiles of 64 keys for
+ * sage_attn_fwd.  Replaces the reference's `v.to(torch.float16)` before the
+ * attention launch (triton_impl.py:189).
+ *
+ *  v        [B,Hkv,Nkv,D] in in_dtype (F32/F16/BF16), strides as above
+ *  pv_mode  SAGE_PV_F16 / SAGE_PV_BF16: round to that type (RNE);
+ *           SAGE_PV_FP8: e4m3 codes RNE_sat(v / v_scale[b,h,d]) (0 where the
+ *           scale is 0), v_scale [B,Hkv,D] from sage_prepass
+ *  out      sage_vtile_bytes() bytes.  Element (b, h, key n, channel d) sits
+ *           at element index (((b*Hkv + h)*T + n/64)*D + d)*64 + pos(n%64),
+ *           T = ceil(Nkv/64), pos(32t + 8i + 4j + r) = 32j + 16t + 4i + r;
+ *           keys past Nkv hold 0.
+ */
+int sage_vtiles(const void* v, int in_dtype, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D,
+                const int64_t* v_strides, int pv_mode, const float* v_scale, void* out,
+                size_t out_bytes, void* stream);
+
+/*
  * Fused attention: O = softmax2(dequant(Q8 K8^T)) V with an online,
  * base-2 softmax (the log2(e) factor is already folded into q_scale).
  * Replaces the _attn_fwd launch (triton_impl.py:186-199).
  *
  *  q8/q_scale/k8/k_scale  as written by sage_prepass (same blkq, q_sub, blkk)
- *  v      [B,Hkv,Nkv,D] in v_dtype (F32/F16/BF16, or FP8E4M3 with v_scale)
+ *  v      the V tiles of sage_vtiles() for the same pv_mode (v_dtype must be
+ *         SAGE_DTYPE_VTILES; v_strides is not read and may be NULL);
+ *         v_scale [B,Hkv,D] with SAGE_PV_FP8
  *  o      [B,Hq,Nq,D] in o_dtype (F32/F16/BF16)
  *  causal 1: key j is visible to query i iff j <= i (top-left aligned, the
  *         torch.tril mask of reference.py:19-22)

@@ -14,6 +14,8 @@ Functions and the reference lines they restate:
   reduction order is the build's definition (sage_quant_math.h)
 * :func:`e4m3_encode` / :func:`quant_v_fp8`  FP8 V (absent in the reference;
   OCP e4m3 as torch.float8_e4m3fn, RNE, saturating)
+* :func:`vtiles`                the build's V tile layout of the attention
+  kernel (V converted as triton_impl.py:189, v.to(torch.float16))
 * :func:`sdpa`                  reference.py:15-24 (+ GQA, chunked)
 * :func:`sage_emulate`          triton_impl.py:86-160 in exact arithmetic:
   dequantized int8 scores, exact softmax, fp64 P.V
@@ -200,6 +202,33 @@ def quant_v_fp8(v):
         t = v / vs[:, :, None, :]
     t = np.where(vs[:, :, None, :] > 0, t, np.float32(0.0)).astype(np.float32)
     return e4m3_encode(t), vs
+
+
+def vtile_positions() -> np.ndarray:
+    """pos[k] of key k (0..63) inside a V tile: k = 32t + 8i + 4h + r -> 32h + 16t + 4i + r.
+
+    The build's own layout (the order in which lane half h of a 32x32 MFMA C
+    tile holds the keys of its column), documented in include/sage_attn.h.
+    """
+    k = np.arange(64)
+    t, i, h, r = k >> 5, (k >> 3) & 3, (k >> 2) & 1, k & 3
+    return 32 * h + 16 * t + 4 * i + r
+
+
+def vtiles(v_elems):
+    """Tile layout of per-element values [B, H, N, D] (any dtype, already
+    converted): returns [B, H, ceil(N/64), D, 64] with keys at vtile_positions()
+    and zeros past N.  The V conversion of triton_impl.py:189 (v.to(float16))
+    is the caller's (e.g. numpy astype(float16)); this is only the layout."""
+    v_elems = np.asarray(v_elems)
+    B, H, N, D = v_elems.shape
+    T = -(-N // 64)
+    pad = np.zeros((B, H, T * 64, D), dtype=v_elems.dtype)
+    pad[:, :, :N] = v_elems
+    tiles = pad.reshape(B, H, T, 64, D).transpose(0, 1, 2, 4, 3)  # [B,H,T,D,key]
+    out = np.zeros_like(tiles)
+    out[..., vtile_positions()] = tiles
+    return out
 
 
 # --------------------------------------------------------------------------

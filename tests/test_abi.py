@@ -25,7 +25,7 @@ def lib(hip_impl):
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_last_error", "sage_prepass",
-                                     "sage_prepass_workspace_bytes"]
+                                     "sage_prepass_workspace_bytes", "sage_vtile_bytes", "sage_vtiles"]
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -82,6 +82,26 @@ def test_attn_rejects_bad_arguments(lib):
     rc = lib.sage_attn_fwd(p, s3, p, p, s3, p, p, 2, s3, None, p, 1, s3, 1, 2, 2, 64, 64, 64, 0, 128, 64, 128, 0,
                            None)
     assert rc != 0 and "v_dtype" in lib.sage_last_error().decode()
+
+
+def test_vtile_bytes_and_rejections(lib):
+    # tiles of 64 keys (ragged N rounded up), 2 bytes per element for fp16/bf16, 1 for e4m3
+    assert lib.sage_vtile_bytes(4, 32, 4096, 128, 0) == 4 * 32 * 64 * 128 * 64 * 2
+    assert lib.sage_vtile_bytes(2, 8, 17776, 64, 1) == 2 * 8 * 278 * 64 * 64 * 2
+    assert lib.sage_vtile_bytes(1, 32, 32768, 128, 2) == 32 * 512 * 128 * 64
+    assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 0, 2) == 4 * 32 * 16 * 128 * 4
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    p = ctypes.c_void_p(16)
+    big = ctypes.c_size_t(1 << 40)
+    for args, needle in [
+        ((p, 2, 1, 2, 64, 96, s3, 0, None, p, big, None), "head_dim"),
+        ((p, 2, 1, 2, 64, 64, s3, 2, None, p, big, None), "null"),
+        ((p, 2, 1, 2, 64, 64, s3, 5, None, p, big, None), "pv_mode"),
+        ((p, 2, 1, 2, 64, 64, s3, 0, None, p, ctypes.c_size_t(64), None), "out"),
+    ]:
+        rc = lib.sage_vtiles(*args)
+        msg = lib.sage_last_error().decode()
+        assert rc != 0 and "invalid argument" in msg and needle in msg, msg
 
 
 def test_hip_variant_refuses_cpu_tensors(hip_impl):

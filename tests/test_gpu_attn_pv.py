@@ -56,13 +56,13 @@ def test_pv_modes_exact(pv, D, causal, hip_impl, gpu_device):
     q = torch.zeros((B, Hq, N, D), dtype=torch.float32, device=gpu_device)
     k = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=gpu_device)
     if pv == "fp8":
+        # v = codes' values times power-of-two channel scales: the V tiles hold exactly these codes
         codes = O.e4m3_encode(vint)
         assert np.array_equal(O.e4m3_decode(codes), vint)
         vs = (2.0 ** (np.arange(D) % 3 - 1)).astype(np.float32)
         v_scale = np.broadcast_to(vs, (B, Hkv, D)).copy()
-        pre["v8"] = torch.from_numpy(codes).to(gpu_device)
         pre["v_scale"] = torch.from_numpy(v_scale).to(gpu_device)
-        v = torch.zeros((B, Hkv, N, D), dtype=torch.float32, device=gpu_device)
+        v = torch.from_numpy(vint * vs).to(gpu_device)
         emu = O.sage_emulate(q8, np.ones((B, Hq, nqs)), k8, np.ones((B, Hkv, -(-N // 64))), codes,
                              causal=causal, q_sub=q_sub, v_scale=v_scale)
     else:
@@ -107,7 +107,8 @@ def test_fp8_pv_small(case, pack_ref, hip_impl, gpu_device):
     torch.cuda.synchronize()
     got = o.float().cpu().numpy().astype(np.float64)
     assert np.isfinite(got).all()
-    v8, vsc = pre["v8"].cpu().numpy(), pre["v_scale"].cpu().numpy()
+    v8, vsc = O.quant_v_fp8(inp["v"].float().numpy())
+    assert np.array_equal(pre["v_scale"].cpu().numpy(), vsc)  # the pre-pass's per-channel scales, bit-exact
     emu = O.sage_emulate(pre["q8"].cpu().numpy(), pre["q_scale"].cpu().numpy(), pre["k8"].cpu().numpy(),
                          pre["k_scale"].cpu().numpy(), v8, causal=causal, q_sub=hip_impl.WAVE_ROWS, v_scale=vsc)
     want = O.sdpa(inp["q"].float().numpy(), inp["k"].float().numpy(), inp["v"].float().numpy(), causal=causal)

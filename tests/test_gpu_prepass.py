@@ -134,3 +134,49 @@ def test_prepass_special_blocks(hip_impl, gpu_device):
     assert wks[0, 0, 0] == 0.0 and wks[0, 0, 1] == 1.0
     row = gk8[0, 0, 64]
     assert list(row[:10]) == [127, 1, -1, 2, -3, 1, -1, 0, 0, -127]
+
+
+# V tiles (sage_vtiles): the reference's v.to(torch.float16) (triton_impl.py:189),
+# in the attention kernel's tile layout; bit-exact against numpy's conversion
+# (round to nearest even) and the oracle's layout, or the oracle's FP8 codes.
+VT_CASES = [
+    (1, 2, 256, 64, "fp32", "fp16"),
+    (2, 2, 300, 128, "bf16", "fp16"),   # ragged tail: zero keys past N
+    (1, 3, 1000, 128, "fp16", "bf16"),
+    (1, 2, 777, 64, "bf16", "bf16"),
+    (2, 1, 333, 128, "bf16", "fp8"),
+    (1, 2, 200, 64, "fp16", "fp8"),
+]
+
+
+@pytest.mark.parametrize("case", VT_CASES, ids=lambda c: f"B{c[0]}H{c[1]}N{c[2]}D{c[3]}-{c[4]}-to-{c[5]}")
+def test_vtiles_bitexact(case, pack_ref, hip_impl, gpu_device):
+    B, H, N, D, dtype, pv = case
+    print(f"[vtiles] {case}", flush=True)
+    inp = _inputs(pack_ref, B, H, H, N, D, dtype, 0.0, "student_t" if pv == "fp8" else "normal")
+    v = inp["v"].to(gpu_device)
+    v32 = _np32(inp["v"])
+    if pv == "fp8":
+        codes, vs = O.quant_v_fp8(v32)
+        out = hip_impl.vtiles(v, "fp8", torch.from_numpy(vs).to(gpu_device))
+        want = O.vtiles(codes)
+        got = out.cpu().numpy()
+    else:
+        out = hip_impl.vtiles(v, pv)
+        if pv == "fp16":
+            want = O.vtiles(v32.astype(np.float16)).view(np.uint16)
+        else:  # bf16: round to nearest even through torch's own conversion
+            want = O.vtiles(torch.from_numpy(v32).to(torch.bfloat16).view(torch.int16).numpy()).view(np.uint16)
+        got = out.cpu().numpy().view(np.uint16)
+    torch.cuda.synchronize()
+    assert got.size == want.size
+    assert np.array_equal(got.reshape(want.shape), want)
+
+
+def test_vtiles_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
+    inp = _inputs(pack_ref, 2, 3, 3, 250, 128, "bf16", 0.0, "normal", seed=2)
+    v = inp["v"].to(gpu_device)
+    a = hip_impl.vtiles(v, "fp16")
+    b = hip_impl.vtiles(v.transpose(1, 2).contiguous(), "fp16", tensor_layout="NHD")
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

@@ -314,3 +314,23 @@ def test_work_formulas_match_baseline_table():
 
 def test_float32_struct_helper():
     assert struct.unpack("<f", struct.pack("<I", 0x3F800000))[0] == 1.0
+
+
+def test_vtile_layout_round_trip_and_positions():
+    """The V tile layout: positions are a permutation, every lane half holds
+    its 32 keys contiguously, and the tiles decode back to the input with
+    zeros past N."""
+    pos = O.vtile_positions()
+    assert sorted(pos.tolist()) == list(range(64))
+    # register v of key tile t in lane half h holds key 32t + 8(v//4) + 4h + v%4 at column 32h + 16t + v
+    for t in range(2):
+        for h in range(2):
+            for v in range(16):
+                assert pos[32 * t + 8 * (v // 4) + 4 * h + v % 4] == 32 * h + 16 * t + v
+    x = np.arange(2 * 3 * 130 * 8, dtype=np.float32).reshape(2, 3, 130, 8) + 1
+    t = O.vtiles(x)
+    assert t.shape == (2, 3, 3, 8, 64)
+    back = np.zeros((2, 3, 192, 8), np.float32)
+    for k in range(64):
+        back[:, :, k::64, :][:, :, :3] = t[..., pos[k]]
+    assert np.array_equal(back[:, :, :130], x) and not back[:, :, 130:].any()

@@ -39,6 +39,7 @@ UNIT_FLAGS = {
     "sage_prepass.hip": ["-ffp-contract=off"],
     "sage_attn_fwd.hip": [],
     "sage_abi.hip": [],
+    "sage_vtiles.hip": ["-ffp-contract=off"],
 }
 
 

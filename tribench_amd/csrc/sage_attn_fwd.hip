@@ -12,21 +12,21 @@
 // triton_impl.py:137,145,147) are handled here.
 //
 // Organisation (CDNA4):
-//  * A work-group covers 256 query rows of one (batch, head).  The launched
-//    shape is 8 waves (2 per SIMD) of 32 rows each (one 32-row MFMA tile,
-//    QT = 1): Q8 rows, S, P and the O^T accumulators (fp32, 32 x D) all live
-//    in arch VGPRs.  The kernel also builds as 4 waves of 64 rows (QT = 2, O
-//    in the accumulation registers, Q8 read from LDS), which halves LDS
-//    operand traffic but leaves the compiler copying accumulators between
-//    register files.
-//  * K8 and V^T tiles of 64 keys are staged through LDS for all the waves:
-//    the loads of tile j+2 are issued at the top of iteration j and written to
-//    LDS at its end (2 K buffers, 4 V^T buffers, one barrier per iteration).
-//    V is transposed (and converted to the P.V type) while staged.
+//  * A work-group is 8 waves (2 per SIMD) of 32 query rows (one 32-row MFMA
+//    tile each) of one (batch, head): Q8 rows, S, P and the O^T accumulators
+//    (fp32, 32 x D) all live in arch VGPRs.
+//  * K8 rows and V^T rows reach LDS in tiles of 64 keys by direct global ->
+//    LDS loads (global_load_lds_dwordx4), three tiles ahead of their use, in a
+//    ring of 5 slots: no staging registers and no VALU work.  V arrives
+//    already converted and transposed (sage_vtiles), so a tile is a plain
+//    copy.  The 16-byte chunks of each LDS row are XOR-swizzled so that the
+//    operand reads of 16 consecutive lanes (rows) hit distinct banks.
+//  * Each wave waits (vmcnt) for exactly its own loads of the tile the next
+//    iteration reads, then meets the others at a barrier without a memory
+//    fence (__syncthreads' fence would drain the whole prefetch).
 //  * Software pipeline inside each wave: iteration j runs the P.V MFMAs of
 //    block j-1 together with the softmax of block j (VALU), then the QK MFMAs
-//    of block j+1, so the matrix cores and the vector ALUs work at the same
-//    time.  Blocks that need no mask take a path with no masking code.
+//    of block j+1.  Blocks that need no mask take a path with no masking code.
 //  * The i32 score accumulator starts at the bit pattern of 2^23 + 2^22, so
 //    it reads as the float 12582912 + S (exact for |S| < 2^22 >= 127^2 * D):
 //    dequantisation and max-subtraction are one FMA per score.
@@ -36,13 +36,11 @@
 //    iteration, once the P.V MFMAs of the previous block have retired.
 //  * The MFMA C layout (lane 32h + n holds column n, rows 8i + 4h + r) is used
 //    as the B operand of the P.V product directly: P never leaves
-//    registers.  V^T columns are stored in LDS in the order in which a lane
-//    half holds the keys, so each A operand is one or two ds_read_b128.
+//    registers.  The V tiles store keys in the order a lane half holds them,
+//    so each A operand is one or two ds_read_b128.
 //  * Work-group ids are remapped so that all q-blocks of one (batch, head)
 //    run on one XCD (shared L2): the hardware deals work-groups to the 8 XCDs
 //    round-robin.
-#include <stdlib.h>
-
 #include "sage_device.h"
 
 namespace sage {
@@ -56,20 +54,18 @@ struct AttnArgs {
   const float* q_scale;
   const int8_t* k8;
   const float* k_scale;
-  const void* v;
+  const void* v;          // V tiles (sage_vtiles layout)
   const float* v_scale;
   void* o;
-  int64_t sq[2], sk[2], sv[2], so[2];  // batch and head strides (elements)
-  int sqn, skn, svn, son;              // row strides (elements); row offsets fit 32 bits
+  int64_t sq[2], sk[2], so[2];  // batch and head strides (elements)
+  int sqn, skn, son;            // row strides (elements); row offsets fit 32 bits
   int B, Hq, Hkv, Nq, Nkv;
   int causal;
   int q_sub, blkk_shift;  // k scale of key block j: k_scale[j >> blkk_shift]
   int nqs, nks;           // q / k scales per head
 };
 
-constexpr int kBM = 256;  // query rows per work-group
-constexpr int kBN = 64;   // keys per block
-constexpr int kKBuf = 2, kVBuf = 4;
+constexpr int kBN = 64;  // keys per block
 
 // The int32 MFMA accumulator starts at the bit pattern of 2^23 + 2^22.
 constexpr int kMagicI = 0x4B400000;
@@ -167,68 +163,58 @@ __device__ __forceinline__ float sum_halves(float v) {
   return __int_as_float((int)a[0]) + __int_as_float((int)a[1]);
 }
 
-// 4x4 byte transpose: out[i] = byte i of a, b, c, d
-__device__ __forceinline__ void transpose4x4(uint32_t a, uint32_t b, uint32_t c, uint32_t d, uint32_t (&o)[4]) {
-  const uint32_t t0 = __builtin_amdgcn_perm(b, a, 0x05010400u);  // a0 b0 a1 b1
-  const uint32_t t1 = __builtin_amdgcn_perm(b, a, 0x07030602u);  // a2 b2 a3 b3
-  const uint32_t t2 = __builtin_amdgcn_perm(d, c, 0x05010400u);  // c0 d0 c1 d1
-  const uint32_t t3 = __builtin_amdgcn_perm(d, c, 0x07030602u);  // c2 d2 c3 d3
-  o[0] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-  o[1] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-  o[2] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-  o[3] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+// s_waitcnt vmcnt(n) alone (gfx9 encoding: expcnt and lgkmcnt at their maxima)
+#define SAGE_WAIT_VM(n) __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+#define SAGE_WAIT_LGKM0() __builtin_amdgcn_s_waitcnt(0xC07F)
+
+// Work-group barrier without the memory fence of __syncthreads(): the fence
+// would drain every direct-to-LDS load in flight, i.e. the whole prefetch.
+// Callers wait for exactly the loads and LDS reads that must be complete.
+__device__ __forceinline__ void wg_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
-// LDS column of the 4-key group kg (keys 4kg..4kg+3) of a V^T tile, in units
-// of 4 keys.  Key 32t + 8i + 4h + r sits at S^T row i*8 + 4h + r of key tile t,
-// i.e. in register 4i + r of lane half h; lane half h reads its 32 keys
-// contiguously from column 32h + 16t + 4i + r.
-__device__ __forceinline__ int vcol4(int kg) { return 8 * (kg & 1) + 4 * (kg >> 3) + ((kg >> 1) & 3); }
+// XOR swizzle of the 16-byte chunks of an LDS row of RB bytes: chunk c of row
+// r is stored at chunk c ^ swz<RB>(r).  For a column read by 16 consecutive
+// lanes (16 consecutive rows), every lane then hits its own 4 banks.
+template <int RB>
+__device__ __forceinline__ int swz(int r) {
+  return (r / (256 / RB)) & (RB / 16 - 1);
+}
 
-// V staging source per P.V mode: TV elements (converted) or e4m3 codes
-template <typename TV, int PVM>
-struct VStage {
-  Raw8<TV> r[4];  // 4 keys x 8 channels
-};
-template <typename TV>
-struct VStage<TV, SAGE_PV_FP8> {
-  uint4 r[4];  // 4 keys x 16 channels of e4m3 codes
-};
+typedef __attribute__((address_space(1))) const void gmem_t;
+typedef __attribute__((address_space(3))) void lmem_t;
 
-// QT 32-row q tiles per wave: QT = 1 -> 8 waves (2 per SIMD), everything in
-// arch VGPRs; QT = 2 -> 4 waves (1 per SIMD), O in the accumulation registers.
-template <int D, int QT, typename TV, int PVM, typename TO>
-__global__ __launch_bounds__(512 / QT) __attribute__((amdgpu_waves_per_eu(2 / QT, 2 / QT))) void attn_fwd_kernel(
-    AttnArgs a) {
-  constexpr int NW = 8 / QT;      // waves per work-group
-  constexpr int NT = 64 * NW;     // threads per work-group
-  constexpr int QW = 32 * QT;     // query rows per wave
-  constexpr bool kQReg = QT == 1; // Q8 operand kept in registers (else read from LDS)
+// One work-group: 8 waves (2 per SIMD) of 32 query rows (one 32-row MFMA tile
+// each) of one (batch, head); Q8 rows, S, P and the O^T accumulators live in
+// arch VGPRs.  Tiles of 64 keys (K8 rows and V^T rows) reach LDS by direct
+// global -> LDS loads, three tiles ahead of their use, in a ring of 5.
+template <int D, int PVM, typename TO>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(AttnArgs a) {
+  constexpr int NW = 8;
+  constexpr int BM = 256;  // query rows per work-group
   constexpr bool kF8 = PVM == SAGE_PV_FP8;
   using Pv = PvT<PVM>;
-  constexpr int KC = D / 32;          // 32-byte slices of the QK contraction
-  constexpr int DT = D / 32;          // 32-row d tiles of O^T
-  constexpr int PW = Pv::kPW;         // P dwords per lane per q tile
-  constexpr int KP = D + 16;          // K8 tile row pitch (bytes)
-  constexpr int VP = 64 * Pv::kEB + 16;  // V^T tile row pitch (bytes)
-  constexpr int KTB = kBN * KP;
-  constexpr int VTB = D * VP;
-  constexpr int KCPR = D / 16;        // 16-byte chunks per K8 row
-  constexpr int KCH = kBN * KCPR;     // 16-byte chunks per K8 tile
-  constexpr int KCH_T = (KCH + NT - 1) / NT;
-  constexpr int VCW = kF8 ? 16 : 8;   // channels per V micro-tile (4 keys each)
-  constexpr int VMT = (kBN / 4) * (D / VCW);  // V micro-tiles per tile
-  static_assert(KCH % NT == 0 || KCH < NT, "K staging");
-  static_assert(VMT <= NT, "V staging: one micro-tile per thread");
+  constexpr int EB = Pv::kEB;
+  constexpr int KC = D / 32;        // 32-byte slices of the QK contraction
+  constexpr int DT = D / 32;        // 32-row d tiles of O^T
+  constexpr int PW = Pv::kPW;       // P dwords per lane
+  constexpr int KRB = D;            // K8 row bytes
+  constexpr int VRB = 64 * EB;      // V^T row bytes
+  constexpr int KTB = kBN * KRB;    // K8 tile bytes
+  constexpr int VTB = D * VRB;      // V^T tile bytes
+  constexpr int SLOT = KTB + VTB;
+  constexpr int NBUF = 5;           // tiles j-1 .. j+3 of iteration j
+  constexpr int KLD = KTB / 1024;   // 1 KB wave loads per K8 tile
+  constexpr int VLD = VTB / 1024;
+  constexpr int LPW = (KLD + VLD + NW - 1) / NW;  // wave loads per wave per tile
+  static_assert(LPW * NW >= KLD + VLD && LPW <= 15, "tile loads");
 
-  constexpr int QTB = kQReg ? 0 : kBM * KP;  // bytes of the work-group's Q8 rows in LDS
-  __shared__ __attribute__((aligned(16))) char smem[QTB + kKBuf * KTB + kVBuf * VTB];
-  __shared__ float ksc_s[kKBuf];
-  char* const qbuf = smem;
-  char* const kbuf0 = smem + QTB;
-  char* const vbuf0 = smem + QTB + kKBuf * KTB;
+  __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT + 1024];  // + a sink for spare loads
 
-  const int nqb = (a.Nq + kBM - 1) / kBM;
+  const int nqb = (a.Nq + BM - 1) / BM;
   const int wg = remap_xcd((int)blockIdx.x, (int)gridDim.x);
   int qb = wg % nqb;
   const int h = (wg / nqb) % a.Hq;
@@ -240,187 +226,141 @@ __global__ __launch_bounds__(512 / QT) __attribute__((amdgpu_waves_per_eu(2 / QT
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int hh = lane >> 5, n = lane & 31;
-  const int q0 = qb * kBM;
-  const int qa = q0 + wave * QW;  // first q row of this wave
+  const int q0 = qb * BM;
+  const int qa = q0 + wave * 32;  // first q row of this wave
 
   const int8_t* qbase = a.q8 + b * a.sq[0] + h * a.sq[1];
   const int8_t* kbase = a.k8 + b * a.sk[0] + hk * a.sk[1];
-  const float* ksc_base = a.k_scale + ((int64_t)b * a.Hkv + hk) * a.nks;
+  // k scales are read through the constant address space (scalar loads, which
+  // the tile-load accounting on vmcnt does not see); the kernel never writes them
+  typedef __attribute__((address_space(4))) const float cfloat_t;
+  cfloat_t* ksc_base = (cfloat_t*)(a.k_scale + ((int64_t)b * a.Hkv + hk) * a.nks);
+  const int ntile = (a.Nkv + kBN - 1) / kBN;
+  const uint8_t* vtbase = static_cast<const uint8_t*>(a.v) + ((int64_t)b * a.Hkv + hk) * ntile * (int64_t)VTB;
 
-  // ---- Q8 (B operand of S^T = K Q^T): rows qa + 32s + n, bytes 32c + 16hh.
-  // Held in registers (QT = 1) or staged in LDS for the work-group (row pitch
-  // KP).  Rows past Nq read the last row; their results are never stored.
-  v4i qreg[QT][KC];
-  if constexpr (kQReg) {
+  // ---- Q8, the B operand of S^T = K Q^T: row qa + n, bytes 32c + 16hh .. +16.
+  // Rows past Nq read the last row; their results are never stored.
+  v4i qreg[KC];
+  {
+    const int row = min(qa + n, a.Nq - 1);
 #pragma unroll
-    for (int s = 0; s < QT; ++s) {
-      const int row = min(qa + 32 * s + n, a.Nq - 1);
-#pragma unroll
-      for (int c = 0; c < KC; ++c)
-        qreg[s][c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 32 * c + 16 * hh));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < (kBM * KCPR) / NT; ++i) {
-      const int L = tid + i * NT;
-      const int row = min(q0 + L / KCPR, a.Nq - 1);
-      *reinterpret_cast<v4i*>(qbuf + (L / KCPR) * KP + 16 * (L % KCPR)) =
-          *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 16 * (L % KCPR)));
-    }
+    for (int c = 0; c < KC; ++c)
+      qreg[c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 32 * c + 16 * hh));
   }
-  float qsc[QT];
-#pragma unroll
-  for (int s = 0; s < QT; ++s) {
-    const int si = min((qa + 32 * s) / a.q_sub, a.nqs - 1);
-    qsc[s] = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + si];
-  }
+  const float qsc = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)];
 
   // ---- key blocks of the work-group and of this wave
-  const int nkb_all = (a.Nkv + kBN - 1) / kBN;
+  const int nkb_all = ntile;
   int nkb = nkb_all;
-  if (a.causal) nkb = min(nkb_all, (min(q0 + kBM, a.Nq) - 1) / kBN + 1);
-  const int q_last = min(qa + QW, a.Nq) - 1;  // last valid row of this wave (< qa if none)
-  int jmax = nkb - 1;                           // last block this wave computes
+  if (a.causal) nkb = min(nkb_all, (min(q0 + BM, a.Nq) - 1) / kBN + 1);
+  const int q_last = min(qa + 32, a.Nq) - 1;  // last valid row of this wave (< qa if none)
+  int jmax = nkb - 1;                          // last block this wave computes
   if (q_last < qa) jmax = -1;
   else if (a.causal) jmax = min(jmax, q_last / kBN);
   // leading blocks that need no mask: whole 64 keys inside Nkv and, when
   // causal, every key <= the wave's first row
   int nfull = a.Nkv / kBN;
-  if (a.causal) nfull = min(nfull, qa / kBN);
+  if (a.causal) nfull = min(nfull, (qa + 1) / kBN);
   nfull = min(nfull, jmax + 1);
 
-  // ---- staging: K8 chunk L = tid + i*256 -> row L / KCPR, chunk L % KCPR;
-  // V micro-tile m = tid -> keys 4*(m % 16) .. +4, channels VCW*(m / 16) .. +VCW.
-  // Keys past Nkv read the last key: their P is 0 and the data is finite.
-  v4i kst[KCH_T];
-  VStage<TV, PVM> vst;
-  float kscst = 0.0f;
-  const int vkg = tid & 15, vcg = tid >> 4;
+  // ---- tile loads.  Wave load g = wave + 8i (i < LPW) of a tile is the 1 KB
+  // LDS range [1024g, 1024g + 1024) of its slot (K8 rows first, then V^T rows);
+  // lane l brings the 16-byte chunk that lands at offset 16l, i.e. the logical
+  // chunk (physical chunk ^ swizzle of its row).  K8 rows past Nkv read the
+  // last row (their P is 0); V^T tiles are zero past Nkv.  Loads past the
+  // tile go to the sink, so every wave issues LPW loads per tile.
   auto load_tile = [&](int j) __attribute__((always_inline)) {
+    char* slot = smem + (j % NBUF) * SLOT;
     const int k0 = j * kBN;
-    if (tid == 0) kscst = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
+    const uint8_t* vt = vtbase + (int64_t)j * VTB;
 #pragma unroll
-    for (int i = 0; i < KCH_T; ++i) {
-      const int L = tid + i * NT;
-      if (KCH % NT == 0 || L < KCH) {
-        const int row = min(k0 + L / KCPR, a.Nkv - 1);
-        kst[i] = *reinterpret_cast<const v4i*>(kbase + (uint32_t)(row * a.skn + 16 * (L % KCPR)));
-      }
-    }
-    if (VMT == NT || tid < VMT) {
-      if constexpr (kF8) {
-        const uint8_t* vb = static_cast<const uint8_t*>(a.v) + b * a.sv[0] + hk * a.sv[1];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vst.r[r] = *reinterpret_cast<const uint4*>(vb + (uint32_t)(min(k0 + 4 * vkg + r, a.Nkv - 1) * a.svn +
-                                                                      VCW * vcg));
+    for (int i = 0; i < LPW; ++i) {
+      const int g = wave + NW * i;  // wave-uniform
+      const void* src;
+      char* dst;
+      if (g < KLD) {
+        const int p = 64 * g + lane;
+        const int r = p / (KRB / 16), pc = p % (KRB / 16);
+        const int row = min(k0 + r, a.Nkv - 1);
+        src = kbase + (uint32_t)(row * a.skn + 16 * (pc ^ swz<KRB>(r)));
+        dst = slot + 1024 * g;
+      } else if (g < KLD + VLD) {
+        const int p = 64 * (g - KLD) + lane;
+        const int d = p / (VRB / 16), pc = p % (VRB / 16);
+        src = vt + d * VRB + 16 * (pc ^ swz<VRB>(d));
+        dst = slot + KTB + 1024 * (g - KLD);
       } else {
-        const TV* vb = static_cast<const TV*>(a.v) + b * a.sv[0] + hk * a.sv[1];
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          vst.r[r] = load8<TV>(vb + (uint32_t)(min(k0 + 4 * vkg + r, a.Nkv - 1) * a.svn + VCW * vcg));
+        src = kbase;
+        dst = smem + NBUF * SLOT;
       }
+      __builtin_amdgcn_global_load_lds((gmem_t*)src, (lmem_t*)dst, 16, 0, 0);
     }
   };
-  auto store_tile = [&](int j) __attribute__((always_inline)) {
-    char* ks = kbuf0 + (j & 1) * KTB;
-    char* vs = vbuf0 + (j & 3) * VTB;
-    if (tid == 0) ksc_s[j & 1] = kscst;
-#pragma unroll
-    for (int i = 0; i < KCH_T; ++i) {
-      const int L = tid + i * NT;
-      if (KCH % NT == 0 || L < KCH)
-        *reinterpret_cast<v4i*>(ks + (L / KCPR) * KP + 16 * (L % KCPR)) = kst[i];
-    }
-    if (VMT == NT || tid < VMT) {
-      char* dst = vs + VCW * vcg * VP + 4 * Pv::kEB * vcol4(vkg);
-      if constexpr (kF8) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          uint32_t t[4];
-          transpose4x4(word(vst.r[0], w), word(vst.r[1], w), word(vst.r[2], w), word(vst.r[3], w), t);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) *reinterpret_cast<uint32_t*>(dst + (4 * w + e) * VP) = t[e];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          v2i w = {(int)Pv::pack2(elem<TV>(vst.r[0], e), elem<TV>(vst.r[1], e)),
-                   (int)Pv::pack2(elem<TV>(vst.r[2], e), elem<TV>(vst.r[3], e))};
-          *reinterpret_cast<v2i*>(dst + e * VP) = w;
-        }
-      }
-    }
+  // end of an iteration: this wave's loads of the tile needed next are done
+  // (at most `ahead` younger tiles in flight), its LDS reads are done, barrier
+  auto sync_tiles = [&](bool ahead) __attribute__((always_inline)) {
+    if (ahead) SAGE_WAIT_VM(LPW);
+    else SAGE_WAIT_VM(0);
+    SAGE_WAIT_LGKM0();
+    wg_barrier();
   };
 
   // ---- accumulators and softmax state
-  v16f oacc[DT][QT];
-  float m_use[QT], lsum[QT], alpha_o[QT];  // lsum: this lane's share of the row sums
+  v16f oacc[DT];
 #pragma unroll
-  for (int s = 0; s < QT; ++s) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) oacc[dt][s] = (v16f){};
-    m_use[s] = -INFINITY;
-    lsum[s] = 0.0f;
-    alpha_o[s] = 1.0f;
-  }
-  bool pend = false;  // O must be multiplied by alpha_o before the next P.V
-  v16i S[2][QT];      // S^T of key tile t, q tile s
-  float ksc_cur = 0.0f;           // k scale of the block held in S
-  uint32_t Pprev[QT][PW], Pcur[QT][PW];  // P of blocks j-1 and j
+  for (int dt = 0; dt < DT; ++dt) oacc[dt] = (v16f){};
+  float m_use = -INFINITY;
+  float lsum = 0.0f;     // this lane's share of the row sum
+  float alpha_o = 1.0f;  // pending factor of O
+  bool pend = false;     // O must be multiplied by alpha_o before the next P.V
+  v16i S[2];             // S^T of key tiles 0 and 1 of the block in flight
+  float ksc_cur = 0.0f;  // k scale of the block held in S
+  uint32_t Pprev[PW], Pcur[PW];  // P of blocks j-1 and j
   const v16i magic = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
                       kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
 
+  // per-lane byte offsets of the swizzled operand chunks
+  int koff[KC];  // K8 row 32t + n (swizzle independent of t), logical chunk 2c + hh
+#pragma unroll
+  for (int c = 0; c < KC; ++c) koff[c] = n * KRB + 16 * ((2 * c + hh) ^ swz<KRB>(n));
+  constexpr int VCH = kF8 ? 2 : 4;  // chunks of a V^T operand read per d tile
+  int voff[VCH];  // V^T row 32dt + n (swizzle independent of dt)
+#pragma unroll
+  for (int c = 0; c < VCH; ++c) voff[c] = KTB + n * VRB + 16 * ((VCH * hh + c) ^ swz<VRB>(n));
+
   // ---- building blocks
-  // S^T of block j (its K8 tile in buffer j & 1)
-  // Q operand (s, c): row 32s + n of the wave's rows, bytes 32c + 16hh .. +16
-  const char* qrd = qbuf + (wave * QW + n) * KP + 16 * hh;
+  // S^T of block j (its K8 tile in slot j % NBUF): K row 32t + n, bytes 32c + 16hh
   auto qk = [&](int j) __attribute__((always_inline)) {
-    const char* ks = kbuf0 + (j & 1) * KTB + n * KP + 16 * hh;
-    ksc_cur = ksc_s[j & 1];
-    v4i qb[QT][KC];
-#pragma unroll
-    for (int s = 0; s < QT; ++s)
-#pragma unroll
-      for (int c = 0; c < KC; ++c)
-        qb[s][c] = kQReg ? qreg[s][c] : *reinterpret_cast<const v4i*>(qrd + 32 * s * KP + 32 * c);
+    const char* ks = smem + (j % NBUF) * SLOT;
+    ksc_cur = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       v4i ka[KC];
 #pragma unroll
-      for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const v4i*>(ks + 32 * t * KP + 32 * c);
+      for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const v4i*>(ks + 32 * t * KRB + koff[c]);
 #pragma unroll
       for (int c = 0; c < KC; ++c)
-#pragma unroll
-        for (int s = 0; s < QT; ++s)
-          S[t][s] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qb[s][c], c == 0 ? magic : S[t][s], 0, 0, 0);
+        S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qreg[c], c == 0 ? magic : S[t], 0, 0, 0);
     }
   };
-  // O^T += V^T P^T of block j (its V^T tile in buffer j & 3)
-  auto pv = [&](int j, const uint32_t (&P)[QT][PW]) __attribute__((always_inline)) {
-    const char* vs = vbuf0 + (j & 3) * VTB + n * VP;
+  // O^T += V^T P^T of block j (its V^T tile in slot j % NBUF)
+  auto pv = [&](int j, const uint32_t (&P)[PW]) __attribute__((always_inline)) {
+    const char* vs = smem + (j % NBUF) * SLOT;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const char* vr = vs + 32 * dt * VP;
+      const char* vr = vs + 32 * dt * VRB;
       if constexpr (kF8) {
-        const v4i lo = *reinterpret_cast<const v4i*>(vr + 32 * hh);
-        const v4i hi = *reinterpret_cast<const v4i*>(vr + 32 * hh + 16);
+        const v4i lo = *reinterpret_cast<const v4i*>(vr + voff[0]);
+        const v4i hi = *reinterpret_cast<const v4i*>(vr + voff[1]);
         const v8i va = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-#pragma unroll
-        for (int s = 0; s < QT; ++s) {
-          const v8i pb = {(int)P[s][0], (int)P[s][1], (int)P[s][2], (int)P[s][3],
-                          (int)P[s][4], (int)P[s][5], (int)P[s][6], (int)P[s][7]};
-          oacc[dt][s] = Pv::mma(va, pb, oacc[dt][s]);
-        }
+        const v8i pb = {(int)P[0], (int)P[1], (int)P[2], (int)P[3], (int)P[4], (int)P[5], (int)P[6], (int)P[7]};
+        oacc[dt] = Pv::mma(va, pb, oacc[dt]);
       } else {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {  // 16-key steps: key tile kk/2, register half kk%2
-          const v4i va = *reinterpret_cast<const v4i*>(vr + 64 * hh + 16 * kk);
-#pragma unroll
-          for (int s = 0; s < QT; ++s) {
-            const v4i pb = {(int)P[s][4 * kk], (int)P[s][4 * kk + 1], (int)P[s][4 * kk + 2], (int)P[s][4 * kk + 3]};
-            oacc[dt][s] = Pv::mma(va, pb, oacc[dt][s]);
-          }
+          const v4i va = *reinterpret_cast<const v4i*>(vr + voff[kk]);
+          const v4i pb = {(int)P[4 * kk], (int)P[4 * kk + 1], (int)P[4 * kk + 2], (int)P[4 * kk + 3]};
+          oacc[dt] = Pv::mma(va, pb, oacc[dt]);
         }
       }
     }
@@ -432,102 +372,78 @@ __global__ __launch_bounds__(512 / QT) __attribute__((amdgpu_waves_per_eu(2 / QT
   auto key_ok = [&](int key, int qrow) __attribute__((always_inline)) {
     return key < a.Nkv && (!a.causal || key <= qrow);
   };
-  // softmax of block j held in S -> P (and the running max / sums)
-  auto softmax = [&](int j, uint32_t (&P)[QT][PW], bool masked) __attribute__((always_inline)) {
+  // softmax of block j held in S -> P (and the running max / sums).  Max and
+  // sum are pairwise trees, not serial chains, to keep dependency depth low.
+  auto softmax = [&](int j, uint32_t (&P)[PW], bool masked) __attribute__((always_inline)) {
     const int k0 = j * kBN;
+    const int qrow = qa + n;
+    const float c = qsc * ksc_cur;
+    int x[32];
 #pragma unroll
-    for (int s = 0; s < QT; ++s) {
-      const int qrow = qa + 32 * s + n;
-      const float c = qsc[s] * ksc_cur;
-      int mx = INT_MIN;
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          int x = S[t][s][v];
-          if (masked) x = key_ok(k0 + key_of(t, v), qrow) ? x : INT_MIN;
-          mx = max(mx, x);
-        }
-      mx = max_halves(mx);
-      const float mblk = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * c;
-      // lazy max update (per q column; both lane halves agree)
-      const bool need = mblk > m_use[s] + SoftmaxCfg<PVM>::kTau;
-      const float mnew = need ? mblk : m_use[s];
-      const float alpha = need ? __builtin_amdgcn_exp2f(m_use[s] - mnew) : 1.0f;
-      m_use[s] = mnew;
-      lsum[s] *= alpha;
-      alpha_o[s] *= alpha;
-      pend |= __builtin_amdgcn_ballot_w64(need) != 0;
-      const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
-      const float bias = __builtin_fmaf(kMagicF, c, m);  // x = (2^23+2^22+S)*c - bias = S*c - m
-      float ls = 0.0f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        float p[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(S[t][s][v]), c, -bias));
-          if (masked) e = key_ok(k0 + key_of(t, v), qrow) ? e : 0.0f;
-          p[v] = e;
-          ls += e;
-        }
-        if constexpr (kF8) {
-#pragma unroll
-          for (int w = 0; w < 4; ++w) P[s][4 * t + w] = Pv::pack4(p[4 * w], p[4 * w + 1], p[4 * w + 2], p[4 * w + 3]);
-        } else {
-#pragma unroll
-          for (int w = 0; w < 8; ++w) P[s][8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
-        }
+      for (int v = 0; v < 16; ++v) {
+        x[16 * t + v] = S[t][v];
+        if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = INT_MIN;
       }
-      lsum[s] += ls;
-    }
-  };
-  // scheduling pattern of the fast path: per d tile, its V^T reads, then
-  // each P.V MFMA followed by a share of the softmax VALU work
-  auto interleave = [&]() __attribute__((always_inline)) {
-    constexpr int kMma = kF8 ? QT : 4 * QT;  // MFMAs per d tile
-    constexpr int kRd = kF8 ? 2 : 4;         // ds_read_b128 per d tile
-    constexpr int kValu = (150 * QT + DT * kMma - 1) / (DT * kMma);  // softmax VALU share per MFMA
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      __builtin_amdgcn_sched_group_barrier(0x100, kRd, 0);
+    for (int w = 16; w >= 1; w >>= 1)
 #pragma unroll
-      for (int m = 0; m < kMma; ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);
+      for (int i = 0; i < w; ++i) x[i] = max(x[i], x[i + w]);
+    const int mx = max_halves(x[0]);
+    const float mblk = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * c;
+    // lazy max update (per q column; both lane halves agree)
+    const bool need = mblk > m_use + SoftmaxCfg<PVM>::kTau;
+    const float mnew = need ? mblk : m_use;
+    const float alpha = need ? __builtin_amdgcn_exp2f(m_use - mnew) : 1.0f;
+    m_use = mnew;
+    lsum *= alpha;
+    alpha_o *= alpha;
+    pend |= __builtin_amdgcn_ballot_w64(need) != 0;
+    const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
+    const float bias = __builtin_fmaf(kMagicF, c, m);  // x = (2^23+2^22+S)*c - bias = S*c - m
+    float ls[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float p[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(S[t][v]), c, -bias));
+        if (masked) e = key_ok(k0 + key_of(t, v), qrow) ? e : 0.0f;
+        p[v] = e;
       }
+      if constexpr (kF8) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) P[4 * t + w] = Pv::pack4(p[4 * w], p[4 * w + 1], p[4 * w + 2], p[4 * w + 3]);
+      } else {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) P[8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
+      }
+#pragma unroll
+      for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) p[i] += p[i + w];
+      ls[t] = p[0];
     }
+    lsum += ls[0] + ls[1];
   };
   auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < QT; ++s) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) oacc[dt][s] *= alpha_o[s];
-      alpha_o[s] = 1.0f;
-    }
+    for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha_o;
+    alpha_o = 1.0f;
   };
-
-  // ---- one iteration: P.V of block j-1, softmax of block j, S of block j+1,
-  // staging of tile j+2.  Iteration nkb only finishes the last P.V.
-  // ---- iterations.  Iteration j: P.V of block j-1, softmax of block j, S of
-  // block j+1, staging of tile j+2; iteration nkb only finishes the last P.V.
-  // Every wave runs nkb + 1 iterations (one barrier each).  The mask-free
-  // steady state has a loop of its own so that the O accumulators are
-  // updated from one place in each loop.
   auto keep_p = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < QT; ++s)
-#pragma unroll
-      for (int w = 0; w < PW; ++w) Pprev[s][w] = Pcur[s][w];
+    for (int w = 0; w < PW; ++w) Pprev[w] = Pcur[w];
   };
-  auto finish = [&](int j, bool stage) __attribute__((always_inline)) {
-    if (j + 1 <= jmax) qk(j + 1);
-    if (stage) store_tile(j + 2);
-    __syncthreads();
-  };
+
+  // ---- iterations.  Iteration j: loads of tile j+3, P.V of block j-1,
+  // softmax of block j, S of block j+1, then tile j+2 complete and a barrier.
+  // Iteration nkb only finishes the last P.V.  Every wave runs nkb + 1
+  // iterations.  The mask-free steady state has a loop of its own so that the
+  // O accumulators are updated from one place in each loop.
   auto generic_iter = [&](int j) __attribute__((always_inline)) {
-    const bool stage = j + 2 < nkb;
-    if (stage) load_tile(j + 2);
+    if (j + 3 < nkb) load_tile(j + 3);
     if (pend) {
       rescale_o();
       pend = false;
@@ -539,99 +455,83 @@ __global__ __launch_bounds__(512 / QT) __attribute__((amdgpu_waves_per_eu(2 / QT
       else softmax(j, Pcur, true);
       keep_p();
     }
-    finish(j, stage);
+    if (j + 1 <= jmax) qk(j + 1);
+    sync_tiles(j + 3 < nkb);
   };
-  // blocks 1 <= j < j_fast: P.V of block j-1 (MFMA) interleaved with the
-  // softmax of block j (VALU); S of block j+1 and tile j+2 always exist.
-  // The empty asm statements pin values where the pipeline needs them: P
-  // computed before the QK MFMAs, S written to arch registers, O in the
-  // accumulation registers across iterations.
+  // blocks 1 <= j < j_fast: every stage exists and no mask is needed; the P.V
+  // MFMAs of block j-1 and the softmax VALU work of block j share one basic
+  // block for the scheduler to interleave
   auto fast_iter = [&](int j) __attribute__((always_inline)) {
-    load_tile(j + 2);
+    load_tile(j + 3);
     if (pend) {
       rescale_o();
       pend = false;
     }
     pv(j - 1, Pprev);
     softmax(j, Pcur, false);
-    interleave();
-#pragma unroll
-    for (int s = 0; s < QT; ++s)
-#pragma unroll
-      for (int w = 0; w < PW; ++w) asm volatile("" ::"v"(Pcur[s][w]));
     keep_p();
     qk(j + 1);
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int s = 0; s < QT; ++s) asm volatile("" : "+v"(S[t][s]));
-    store_tile(j + 2);
-    if constexpr (QT == 2) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int s = 0; s < QT; ++s) asm volatile("" : "+a"(oacc[dt][s]));
-    }
-    __syncthreads();
+    sync_tiles(true);
   };
 
-  // ---- prologue: tiles 0 and 1 staged, S of block 0
+  // ---- prologue: tiles 0, 1, 2 requested, 0 and 1 awaited; S of block 0
   load_tile(0);
-  store_tile(0);
-  if (nkb > 1) {
-    load_tile(1);
-    store_tile(1);
-  }
-  __syncthreads();
+  if (nkb > 1) load_tile(1);
+  if (nkb > 2) load_tile(2);
+  sync_tiles(nkb > 2);
   if (jmax >= 0) qk(0);
-  __syncthreads();  // block 0's K8 buffer is restaged in iteration 0
 
-  const int j_fast = min(min(nfull, jmax), nkb - 2);
+  const int j_fast = min(min(nfull, jmax), nkb - 3);
   generic_iter(0);
   int j = 1;
   for (; j < j_fast; ++j) fast_iter(j);
   for (; j <= nkb; ++j) generic_iter(j);
 
-  // ---- epilogue: O / l, store rows q = qa + 32s + n, d = 32dt + 8i + 4hh .. +4
+  // ---- epilogue: O / l, store row q = qa + n, d = 32dt + 8i + 4hh .. +4
   if (pend) rescale_o();
   TO* obase = static_cast<TO*>(a.o) + b * a.so[0] + h * a.so[1];
   const float* vsc = kF8 ? a.v_scale + ((int64_t)b * a.Hkv + hk) * D : nullptr;
+  const float inv = 1.0f / sum_halves(lsum);
+  const int row = qa + n;
+  if (row < a.Nq) {
 #pragma unroll
-  for (int s = 0; s < QT; ++s) {
-    const float inv = 1.0f / sum_halves(lsum[s]);
-    const int row = qa + 32 * s + n;
-    if (row < a.Nq) {
+    for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d0 = 32 * dt + 8 * i + 4 * hh;
-          float4 f = make_float4(inv, inv, inv, inv);
-          if constexpr (kF8) {
-            const float4 vs4 = *reinterpret_cast<const float4*>(vsc + d0);
-            f = make_float4(inv * vs4.x, inv * vs4.y, inv * vs4.z, inv * vs4.w);
-          }
-          const v16f& o = oacc[dt][s];
-          store4<TO>(obase + (uint32_t)(row * a.son + d0), o[4 * i] * f.x, o[4 * i + 1] * f.y, o[4 * i + 2] * f.z,
-                     o[4 * i + 3] * f.w);
+      for (int i = 0; i < 4; ++i) {
+        const int d0 = 32 * dt + 8 * i + 4 * hh;
+        float4 f = make_float4(inv, inv, inv, inv);
+        if constexpr (kF8) {
+          const float4 vs4 = *reinterpret_cast<const float4*>(vsc + d0);
+          f = make_float4(inv * vs4.x, inv * vs4.y, inv * vs4.z, inv * vs4.w);
         }
-    }
+        const v16f& o = oacc[dt];
+        store4<TO>(obase + (uint32_t)(row * a.son + d0), o[4 * i] * f.x, o[4 * i + 1] * f.y, o[4 * i + 2] * f.z,
+                   o[4 * i + 3] * f.w);
+      }
   }
 }
 
-template <int D, typename TV, int PVM, typename TO>
+template <int D, int PVM, typename TO>
 static int launch_cfg(const AttnArgs& a, hipStream_t st) {
-  constexpr int QT = 1;
-  const int64_t nqb = (a.Nq + kBM - 1) / kBM;
+  const int64_t nqb = (a.Nq + 255) / 256;
   const int64_t grid = nqb * a.Hq * a.B;
   if (grid > 0x7FFFFFFF) return fail("sage_attn_fwd: invalid argument: grid too large");
-  hipLaunchKernelGGL((attn_fwd_kernel<D, QT, TV, PVM, TO>), dim3((unsigned)grid), dim3(512 / QT), 0, st, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, PVM, TO>), dim3((unsigned)grid), dim3(512), 0, st, a);
   return check_launch("sage_attn_fwd");
 }
 
-template <typename TV, int PVM, typename TO>
+template <int PVM, typename TO>
 static int launch_d(const AttnArgs& a, int D, hipStream_t st) {
-  return D == 64 ? launch_cfg<64, TV, PVM, TO>(a, st) : launch_cfg<128, TV, PVM, TO>(a, st);
+  return D == 64 ? launch_cfg<64, PVM, TO>(a, st) : launch_cfg<128, PVM, TO>(a, st);
+}
+
+template <typename TO>
+static int launch_pv(const AttnArgs& a, int D, int pv_mode, hipStream_t st) {
+  switch (pv_mode) {
+    case SAGE_PV_F16: return launch_d<SAGE_PV_F16, TO>(a, D, st);
+    case SAGE_PV_BF16: return launch_d<SAGE_PV_BF16, TO>(a, D, st);
+    default: return launch_d<SAGE_PV_FP8, TO>(a, D, st);
+  }
 }
 
 static bool strides_ok(const int64_t* s, int esize) {
@@ -664,24 +564,21 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   if (q_sub < 32 || q_sub % 32 != 0 || blkq % q_sub != 0)
     return fail("sage_attn_fwd: invalid argument: q_sub=%d blkq=%d (q_sub: a multiple of 32 dividing blkq)", q_sub,
                 blkq);
-  if (!q8 || !q_scale || !k8 || !k_scale || !v || !o || !q8_strides || !k8_strides || !v_strides || !o_strides)
+  if (!q8 || !q_scale || !k8 || !k_scale || !v || !o || !q8_strides || !k8_strides || !o_strides)
     return fail("sage_attn_fwd: invalid argument: null pointer");
   if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16 && pv_mode != SAGE_PV_FP8)
     return fail("sage_attn_fwd: invalid argument: pv_mode %d", pv_mode);
   if (!is_float_code(o_dtype)) return fail("sage_attn_fwd: invalid argument: o_dtype %d", o_dtype);
-  if (pv_mode == SAGE_PV_FP8) {
-    if (v_dtype != SAGE_DTYPE_FP8E4M3 || !v_scale)
-      return fail("sage_attn_fwd: invalid argument: FP8 P.V needs e4m3 V codes and v_scale");
-  } else if (v_dtype != o_dtype) {
-    return fail("sage_attn_fwd: invalid argument: v_dtype %d / o_dtype %d", v_dtype, o_dtype);
-  }
-  const int ves = v_dtype == SAGE_DTYPE_F32 ? 4 : (v_dtype == SAGE_DTYPE_FP8E4M3 ? 1 : 2);
+  if (v_dtype != SAGE_DTYPE_VTILES)
+    return fail("sage_attn_fwd: invalid argument: v_dtype %d (V must be in the tile layout of sage_vtiles)",
+                v_dtype);
+  if (pv_mode == SAGE_PV_FP8 && !v_scale)
+    return fail("sage_attn_fwd: invalid argument: FP8 P.V needs v_scale");
   const int oes = o_dtype == SAGE_DTYPE_F32 ? 4 : 2;
   const bool rows32 = Nq * q8_strides[2] + D < 0x7FFFFFFF && Nkv * k8_strides[2] + D < 0x7FFFFFFF &&
-                      Nkv * v_strides[2] + D < 0x7FFFFFFF && Nq * o_strides[2] + D < 0x7FFFFFFF;
+                      Nq * o_strides[2] + D < 0x7FFFFFFF;
   if (!rows32) return fail("sage_attn_fwd: invalid argument: a head's rows must span < 2^31 elements");
-  if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(v_strides, ves) ||
-      !strides_ok(o_strides, oes))
+  if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(o_strides, oes))
     return fail("sage_attn_fwd: invalid argument: strides must keep 16-byte aligned rows");
   if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v | (uintptr_t)o) % 16 != 0)
     return fail("sage_attn_fwd: invalid argument: base pointers must be 16-byte aligned");
@@ -697,12 +594,10 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   for (int i = 0; i < 2; ++i) {
     a.sq[i] = q8_strides[i];
     a.sk[i] = k8_strides[i];
-    a.sv[i] = v_strides[i];
     a.so[i] = o_strides[i];
   }
   a.sqn = (int)q8_strides[2];
   a.skn = (int)k8_strides[2];
-  a.svn = (int)v_strides[2];
   a.son = (int)o_strides[2];
   a.B = (int)B;
   a.Hq = (int)Hq;
@@ -716,21 +611,9 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   a.nks = (int)((Nkv + blkk - 1) / blkk);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int d = (int)D;
-  if (pv_mode == SAGE_PV_FP8) {
-    switch (o_dtype) {
-      case SAGE_DTYPE_F32: return launch_d<uint8_t, SAGE_PV_FP8, float>(a, d, st);
-      case SAGE_DTYPE_F16: return launch_d<uint8_t, SAGE_PV_FP8, _Float16>(a, d, st);
-      default: return launch_d<uint8_t, SAGE_PV_FP8, __bf16>(a, d, st);
-    }
-  }
-  const bool bf = pv_mode == SAGE_PV_BF16;
-  switch (v_dtype) {
-    case SAGE_DTYPE_F32:
-      return bf ? launch_d<float, SAGE_PV_BF16, float>(a, d, st) : launch_d<float, SAGE_PV_F16, float>(a, d, st);
-    case SAGE_DTYPE_F16:
-      return bf ? launch_d<_Float16, SAGE_PV_BF16, _Float16>(a, d, st)
-                : launch_d<_Float16, SAGE_PV_F16, _Float16>(a, d, st);
-    default:
-      return bf ? launch_d<__bf16, SAGE_PV_BF16, __bf16>(a, d, st) : launch_d<__bf16, SAGE_PV_F16, __bf16>(a, d, st);
+  switch (o_dtype) {
+    case SAGE_DTYPE_F32: return launch_pv<float>(a, d, pv_mode, st);
+    case SAGE_DTYPE_F16: return launch_pv<_Float16>(a, d, pv_mode, st);
+    default: return launch_pv<__bf16>(a, d, pv_mode, st);
   }
 }

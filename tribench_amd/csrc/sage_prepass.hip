@@ -31,7 +31,8 @@ struct PrepassArgs {
   int64_t sq8[3], sk8[3], sv8[3];  // output strides
   float q_mul;
   int blkq, blkk, q_sub;
-  int smooth_k, v_fp8;
+  int smooth_k, v_fp8;  // v_fp8: V statistics and v_scale
+  int v_rows;            // also the row-major e4m3 codes v8
   int8_t* q8;
   float* q_scale;
   int8_t* k8;
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs 
   }
   __syncthreads();
   quant_k_role<T, D, NIK>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
-  if (a.v_fp8) {
+  if (a.v_rows) {
     const int64_t row0 = kb * a.blkk;
     const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
     const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1] + row0 * a.sv[2];
@@ -408,7 +409,7 @@ extern "C" size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t N
   const int64_t per = B * Hkv * kstat_num_chunks(Nkv) * D * (int64_t)sizeof(float);
   size_t bytes = 0;
   if (smooth_k) bytes += (size_t)per;
-  if (v_mode == SAGE_V_FP8) bytes += (size_t)per;
+  if (v_mode == SAGE_V_FP8 || v_mode == SAGE_V_FP8_SCALE) bytes += (size_t)per;
   return bytes;
 }
 
@@ -435,21 +436,22 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
     return fail("sage_prepass: invalid argument: blkq=%d blkk=%d (16..256, multiples of 16)", blkq, blkk);
   if (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0 || blkq / q_sub > 16)
     return fail("sage_prepass: invalid argument: q_sub=%d for blkq=%d", q_sub, blkq);
-  if (v_mode != SAGE_V_NONE && v_mode != SAGE_V_FP8)
+  if (v_mode != SAGE_V_NONE && v_mode != SAGE_V_FP8 && v_mode != SAGE_V_FP8_SCALE)
     return fail("sage_prepass: invalid argument: v_mode %d", v_mode);
-  const bool vfp8 = v_mode == SAGE_V_FP8;
+  const bool vfp8 = v_mode != SAGE_V_NONE;  // V statistics and v_scale
+  const bool vrows = v_mode == SAGE_V_FP8;  // row-major codes as well
   if (!q || !k || !q8 || !k8 || !q_scale || !k_scale || !q_strides || !k_strides || !q8_strides ||
       !k8_strides)
     return fail("sage_prepass: invalid argument: null pointer");
   if (smooth_k && !km) return fail("sage_prepass: invalid argument: km is null with smooth_k");
-  if (vfp8 && (!v || !v8 || !v_scale || !v_strides || !v8_strides))
-    return fail("sage_prepass: invalid argument: null V pointer with v_mode FP8");
+  if (vfp8 && (!v || !v_scale || !v_strides || (vrows && (!v8 || !v8_strides))))
+    return fail("sage_prepass: invalid argument: null V pointer with v_mode %d", v_mode);
   const int es = in_dtype == SAGE_DTYPE_F32 ? 4 : 2;
   if (!strides_ok(q_strides, es) || !strides_ok(k_strides, es) || !strides_ok(q8_strides, 1) ||
-      !strides_ok(k8_strides, 1) || (vfp8 && (!strides_ok(v_strides, es) || !strides_ok(v8_strides, 1))))
+      !strides_ok(k8_strides, 1) || (vfp8 && !strides_ok(v_strides, es)) || (vrows && !strides_ok(v8_strides, 1)))
     return fail("sage_prepass: invalid argument: strides must keep 16-byte aligned rows");
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)(vfp8 ? v : nullptr) |
-       (uintptr_t)(vfp8 ? v8 : nullptr)) % 16 != 0)
+       (uintptr_t)(vrows ? v8 : nullptr)) % 16 != 0)
     return fail("sage_prepass: invalid argument: base pointers must be 16-byte aligned");
   const size_t need = sage_prepass_workspace_bytes(B, Hkv, Nkv, D, smooth_k, v_mode);
   if (need > 0 && (!workspace || workspace_bytes < need))
@@ -470,7 +472,7 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
     a.sq8[i] = q8_strides[i];
     a.sk8[i] = k8_strides[i];
     a.sv[i] = vfp8 ? v_strides[i] : 0;
-    a.sv8[i] = vfp8 ? v8_strides[i] : 0;
+    a.sv8[i] = vrows ? v8_strides[i] : 0;
   }
   a.q_mul = q_mul;
   a.blkq = blkq;
@@ -478,6 +480,7 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   a.q_sub = q_sub;
   a.smooth_k = smooth_k ? 1 : 0;
   a.v_fp8 = vfp8 ? 1 : 0;
+  a.v_rows = vrows ? 1 : 0;
   a.q8 = q8;
   a.q_scale = q_scale;
   a.k8 = k8;

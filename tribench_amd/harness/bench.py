@@ -209,6 +209,8 @@ def run_benchmark(
         pre_p50 = _stats(pre_lats)["p50"]
         res.prepass_ms_p50 = pre_p50
         pb = est.get("prepass_bytes")
+        if pb and est.get("vtile_bytes"):
+            pb += est["vtile_bytes"]  # the stage also converts V (v.to(float16))
         if pb:
             res.prepass_gbps = compute_gbps(pb, pre_p50)
             res.prepass_hbm_fraction = res.prepass_gbps / PEAKS_MI355X["hbm_gbps"]

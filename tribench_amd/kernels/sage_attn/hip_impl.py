@@ -7,7 +7,8 @@ buffer with torch on the inputs' device and calls the C ABI of
 ``libsage_attn.so`` (include/sage_attn.h) through ctypes, on torch's current
 stream:
 
-    sage_prepass   per_block_int8 (triton_impl.py:35-82) + K smoothing (+ FP8 V)
+    sage_prepass   per_block_int8 (triton_impl.py:35-82) + K smoothing (+ FP8 V scales)
+    sage_vtiles    v.to(torch.float16) (triton_impl.py:189), in the attention's V tile layout
     sage_attn_fwd  _attn_fwd launch (triton_impl.py:186-199)
 
 There is no CPU or PyTorch fallback: without a ROCm device or without the
@@ -25,12 +26,12 @@ from pathlib import Path
 import numpy as np
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
 
-DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_FP8E4M3 = 0, 1, 2, 3
-V_NONE, V_FP8 = 0, 1
+DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_FP8E4M3, DTYPE_VTILES = 0, 1, 2, 3, 4
+V_NONE, V_FP8, V_FP8_SCALE = 0, 1, 2
 PV_MODES = {"fp16": 0, "bf16": 1, "fp8": 2}
 _TORCH_CODES = {torch.float32: DTYPE_F32, torch.float16: DTYPE_F16, torch.bfloat16: DTYPE_BF16}
 
@@ -73,6 +74,10 @@ def _load():
         vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, p64, p64, p64, f32, i32, i32, i32, i32, i32,
         vp, p64, vp, vp, p64, vp, vp, vp, p64, vp, vp, sz, vp,
     ]
+    lib.sage_vtile_bytes.restype = sz
+    lib.sage_vtile_bytes.argtypes = [i64, i64, i64, i64, i32]
+    lib.sage_vtiles.restype = i32
+    lib.sage_vtiles.argtypes = [vp, i32, i64, i64, i64, i64, p64, i32, vp, vp, sz, vp]
     lib.sage_attn_fwd.restype = i32
     lib.sage_attn_fwd.argtypes = [
         vp, p64, vp, vp, p64, vp, vp, i32, p64, vp, vp, i32, p64, i64, i64, i64, i64, i64, i64, i32,
@@ -148,16 +153,40 @@ def _empty_like_layout(t: torch.Tensor, dtype) -> torch.Tensor:
     return torch.empty_like(t, dtype=dtype, memory_format=torch.preserve_format)
 
 
+def vtiles(v, pv_dtype="fp16", v_scale=None, *, tensor_layout="HND"):
+    """V in the attention kernel's tile layout (uint8 buffer), converted to
+    the P.V type: the counterpart of the reference's v.to(torch.float16)
+    (triton_impl.py:189).  ``pv_dtype`` "fp8" needs the per-channel v_scale
+    [B,Hkv,D] of :func:`prepass`."""
+    lib = _load()
+    if pv_dtype not in PV_MODES:
+        raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
+    B, Hkv, Nkv, D = _dims(v, tensor_layout)
+    mode = PV_MODES[pv_dtype]
+    if pv_dtype == "fp8" and v_scale is None:
+        raise ValueError("sage_attn hip: invalid argument: fp8 V tiles need v_scale")
+    nbytes = lib.sage_vtile_bytes(B, Hkv, Nkv, D, mode)
+    out = torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=v.device)
+    rc = lib.sage_vtiles(_ptr(v), _TORCH_CODES[v.dtype], B, Hkv, Nkv, D, _strides(v, tensor_layout), mode,
+                         _ptr(v_scale), _ptr(out), ctypes.c_size_t(nbytes), _stream(v.device))
+    _check(rc, "sage_vtiles")
+    return out
+
+
 def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smooth_k=True,
-            v_fp8=False, tensor_layout="HND"):
+            v_fp8=False, pv_dtype=None, tensor_layout="HND"):
     """Run the HIP pre-pass; returns a dict of device tensors.
 
     q8/k8 (int8, same layout as q/k), q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)],
-    k_scale [B,Hkv,ceil(Nkv/blkk)], km [B,Hkv,D] (smooth_k), and v8 (e4m3 codes
-    as uint8) + v_scale [B,Hkv,D] (v_fp8).
+    k_scale [B,Hkv,ceil(Nkv/blkk)], km [B,Hkv,D] (smooth_k), v8 (row-major e4m3
+    codes as uint8) + v_scale [B,Hkv,D] (v_fp8), and with ``pv_dtype`` the V
+    tiles ``vt`` that :func:`attention` reads (v_scale too for "fp8").
     """
     lib = _load()
     B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v if v is not None else k, tensor_layout)
+    if pv_dtype is not None and pv_dtype not in PV_MODES:
+        raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
+    v_mode = V_FP8 if v_fp8 else (V_FP8_SCALE if pv_dtype == "fp8" else V_NONE)
     q_sub = blkq if q_sub is None else q_sub
     if sm_scale is None:
         sm_scale = D ** -0.5
@@ -170,16 +199,18 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
     k_scale = torch.empty((B, Hkv, -(-Nkv // blkk)), dtype=torch.float32, device=dev)
     km = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev) if smooth_k else None
     v8 = v_scale = None
+    if v_mode != V_NONE:
+        v_scale = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev)
     if v_fp8:
         v8 = _empty_like_layout(v, torch.uint8)
-        v_scale = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev)
-    ws_bytes = lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), V_FP8 if v_fp8 else V_NONE)
+    ws_bytes = lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), v_mode)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    uses_v = v_mode != V_NONE
     rc = lib.sage_prepass(
-        _ptr(q), _ptr(k), _ptr(v) if v_fp8 else None, _TORCH_CODES[q.dtype], B, Hq, Hkv, Nq, Nkv, D,
+        _ptr(q), _ptr(k), _ptr(v) if uses_v else None, _TORCH_CODES[q.dtype], B, Hq, Hkv, Nq, Nkv, D,
         _strides(q, tensor_layout), _strides(k, tensor_layout),
-        _strides(v, tensor_layout) if v_fp8 else None,
-        q_mul, blkq, blkk, q_sub, int(smooth_k), V_FP8 if v_fp8 else V_NONE,
+        _strides(v, tensor_layout) if uses_v else None,
+        q_mul, blkq, blkk, q_sub, int(smooth_k), v_mode,
         _ptr(q8), _strides(q8, tensor_layout), _ptr(q_scale), _ptr(k8), _strides(k8, tensor_layout),
         _ptr(k_scale), _ptr(km), _ptr(v8), _strides(v8, tensor_layout) if v_fp8 else None, _ptr(v_scale),
         _ptr(ws), ctypes.c_size_t(ws_bytes), _stream(dev),
@@ -190,7 +221,10 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         out["km"] = km
     if v_fp8:
         out["v8"] = v8
+    if v_scale is not None:
         out["v_scale"] = v_scale
+    if pv_dtype is not None:
+        out["vt"] = vtiles(v, pv_dtype, v_scale, tensor_layout=tensor_layout)
     return out
 
 
@@ -199,7 +233,7 @@ def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gr
     """The pre-pass of :func:`run` alone, with run's arguments (the harness
     times it as the ``prepass`` stage to report its HBM rate)."""
     q_sub = WAVE_ROWS if q_gran == "wave" else 128
-    return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, v_fp8=pv_dtype == "fp8",
+    return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, pv_dtype=pv_dtype,
                    tensor_layout=tensor_layout)
 
 
@@ -219,22 +253,24 @@ def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=12
               out=None):
     """Launch the fused attention kernel on the outputs of :func:`prepass`.
 
-    Replaces the _attn_fwd launch of triton_impl.py:186-199.  Returns o with
-    q's shape and dtype (written into ``out`` when given).
+    Replaces the _attn_fwd launch of triton_impl.py:186-199.  V is read from
+    ``pre["vt"]`` (built here from ``v`` when absent).  Returns o with q's
+    shape and dtype (written into ``out`` when given).
     """
     lib = _load()
     if pv_dtype not in PV_MODES:
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
     B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
     o = _empty_like_layout(q, q.dtype) if out is None else out
-    if pv_dtype == "fp8":
-        v_in, v_code, v_str = pre["v8"], DTYPE_FP8E4M3, _strides(pre["v8"], tensor_layout)
-    else:
-        v_in, v_code, v_str = v, _TORCH_CODES[v.dtype], _strides(v, tensor_layout)
+    vt = pre.get("vt")
+    if vt is None:
+        vt = vtiles(v, pv_dtype, pre.get("v_scale"), tensor_layout=tensor_layout)
+    elif vt.numel() < lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype]):
+        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] is not a {pv_dtype} tile buffer")
     rc = lib.sage_attn_fwd(
         _ptr(pre["q8"]), _strides(pre["q8"], tensor_layout), _ptr(pre["q_scale"]),
         _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
-        _ptr(v_in), v_code, v_str, _ptr(pre.get("v_scale")),
+        _ptr(vt), DTYPE_VTILES, None, _ptr(pre.get("v_scale")),
         _ptr(o), _TORCH_CODES[o.dtype], _strides(o, tensor_layout),
         B, Hq, Hkv, Nq, Nkv, D, int(bool(causal)), blkq, blkk, q_sub, PV_MODES[pv_dtype], _stream(q.device),
     )
@@ -265,10 +301,11 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
     blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
     q_sub = WAVE_ROWS if q_gran == "wave" else blkq
     pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k,
-                  v_fp8=pv_dtype == "fp8", tensor_layout=tensor_layout)
+                  pv_dtype=pv_dtype, tensor_layout=tensor_layout)
     o = attention(q, k, v, pre, causal, pv_dtype=pv_dtype, q_sub=q_sub, blkq=blkq, blkk=blkk,
                   tensor_layout=tensor_layout)
     if return_intermediates:
         pre.pop("workspace", None)
+        pre.pop("vt", None)
         return o, pre
     return o
