@@ -16,6 +16,8 @@
 // 16-byte loads, held in registers while the block's max|x| is reduced, then
 // quantized and written with 16-byte stores.  Build with -ffp-contract=off:
 // the element arithmetic must round exactly like the reference's.
+#include <type_traits>
+
 #include "sage_device.h"
 
 namespace sage {
@@ -139,25 +141,33 @@ __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_vali
     scale_dst[tid] = sc;
   }
   __syncthreads();
+  // one wave-uniform choice per block: the fast division when every sub-block
+  // scale allows it (always, short of all-zero or extreme blocks)
+  bool fast_all = true;
+  for (int sb = 0; sb < nsub; ++sb) fast_all = fast_all && fast_div_ok(scl_s[sb]);
+  auto quantize = [&](auto fast_tag) __attribute__((always_inline)) {
+    constexpr bool kFast = decltype(fast_tag)::value;
 #pragma unroll
-  for (int j = 0; j < NI; ++j) {
-    const int it = tid + kPrepassThreads * j;
-    const int row = it / CPR, c = it % CPR;
-    if (it >= nit || row >= rows_valid) continue;
-    const int sub = row / q_sub;
-    const float sc = scl_s[sub], rc = rcp_s[sub];
-    const bool fast = fast_div_ok(sc);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+    for (int j = 0; j < NI; ++j) {
+      const int it = tid + kPrepassThreads * j;
+      const int row = it / CPR, c = it % CPR;
+      if (it >= nit || row >= rows_valid) continue;
+      const int sub = row / q_sub;
+      const float sc = scl_s[sub], rc = rcp_s[sub];
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      float x = elem<T>(raw[j][e >> 3], e & 7);
-      if (use_mul) x = x * mul;
-      if (km_s) x = x - km_s[c * 16 + e];
-      const int8_t qv = quant_elem(x, sc, rc, fast);
-      w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
+      for (int e = 0; e < 16; ++e) {
+        float x = elem<T>(raw[j][e >> 3], e & 7);
+        if (use_mul) x = x * mul;
+        if (km_s) x = x - km_s[c * 16 + e];
+        const int8_t qv = quant_elem(x, sc, rc, kFast);
+        w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
+      }
+      *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
     }
-    *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
+  };
+  if (__builtin_amdgcn_readfirstlane((int)fast_all)) quantize(std::true_type{});
+  else quantize(std::false_type{});
 }
 
 // ---------------------------------------------------------------------------

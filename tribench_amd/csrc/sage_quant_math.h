@@ -38,7 +38,9 @@ SAGE_HD inline float div_rn(float x, float scale, float rcp) {
 // The reference's rounding (triton_impl.py:29-31): t += 0.5*sign(t) in fp32,
 // then truncate toward zero.  Note fp32(0.49999997 + 0.5) == 1.0.
 SAGE_HD inline int round_half_away(float t) {
-  float u = t + (t >= 0.0f ? 0.5f : -0.5f);
+  // copysign(0.5, t) equals (t >= 0 ? 0.5 : -0.5) except at t = -0, where
+  // -0 - 0.5 and -0 + 0.5 both truncate to 0
+  float u = t + __builtin_copysignf(0.5f, t);
   return (int)u;
 }
 
