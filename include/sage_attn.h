@@ -135,7 +135,7 @@ int sage_vtiles(const void* v, int in_dtype, int64_t B, int64_t Hkv, int64_t Nkv
  *  causal 1: key j is visible to query i iff j <= i (top-left aligned, the
  *         torch.tril mask of reference.py:19-22)
  *  GQA    query head h reads KV head h / (Hq/Hkv) (triton_impl.py:137,145,147)
- *  blkk must be a multiple of 64, q_sub a multiple of 16.
+ *  blkk must be 64, 128 or 256; q_sub a multiple of 32 that divides blkq.
  */
 int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_scale,
                   const int8_t* k8, const int64_t* k8_strides, const float* k_scale,

@@ -102,6 +102,48 @@ def test_attn_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
     assert torch.equal(o1, o2.transpose(1, 2))
 
 
+# Nq != Nkv (the reference's per_block_int8 takes them separately, triton_impl.py:43-44):
+# cross attention and a decode-like single query row; causal is top-left
+# (key j visible to query i iff j <= i), so rows >= Nkv see every key.
+# (B, Hq, Hkv, Nq, Nkv, D, causal)
+CROSS = [
+    (1, 4, 2, 200, 777, 128, False),
+    (2, 2, 2, 1000, 64, 64, False),
+    (1, 2, 1, 1, 500, 128, False),
+    (1, 2, 2, 300, 129, 64, True),
+    (1, 2, 1, 130, 700, 128, True),
+]
+
+
+@pytest.mark.parametrize("case", CROSS, ids=lambda c: f"B{c[0]}Hq{c[1]}Hkv{c[2]}Nq{c[3]}Nkv{c[4]}D{c[5]}c{int(c[6])}")
+def test_attn_cross_lengths(case, hip_impl, gpu_device):
+    B, Hq, Hkv, Nq, Nkv, D, causal = case
+    print(f"[attn-cross] {case}", flush=True)
+    g = torch.Generator().manual_seed(Nq * 7 + Nkv)
+    q = torch.randn(B, Hq, Nq, D, generator=g)
+    k = torch.randn(B, Hkv, Nkv, D, generator=g) + 2.0 * torch.randn(B, Hkv, 1, D, generator=g)
+    v = torch.randn(B, Hkv, Nkv, D, generator=g)
+    qb, kb, vb = (t.to(torch.bfloat16) for t in (q, k, v))
+    o, pre = hip_impl.run(qb.to(gpu_device), kb.to(gpu_device), vb.to(gpu_device), causal=causal,
+                          return_intermediates=True)
+    torch.cuda.synchronize()
+    assert o.shape == (B, Hq, Nq, D)
+    got = o.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    qf, kf, vf = (t.float().numpy() for t in (qb, kb, vb))
+    want = O.sdpa(qf, kf, vf, causal=causal)
+    emu = O.sage_emulate(pre["q8"].cpu().numpy(), pre["q_scale"].cpu().numpy(), pre["k8"].cpu().numpy(),
+                         pre["k_scale"].cpu().numpy(), vf, causal=causal)
+    quant_err, _ = _metrics(emu, want)
+    max_abs, cos = _metrics(got, want)
+    print(f"  kernel vs fp64 SDPA: max_abs={max_abs:.3e} cos={cos:.6f} (emulation vs SDPA: {quant_err:.3e})")
+    assert _vs_emulation(got, emu, torch.bfloat16) <= EMUL_ABS
+    slack = EMUL_ABS + OUT_EPS[torch.bfloat16] * float(np.abs(emu).max())
+    # rows that see fewer than 128 keys keep the emulation's own error (module docstring)
+    bound = MAX_ABS if (not causal and Nkv >= 128) else max(MAX_ABS, quant_err + slack)
+    assert max_abs <= bound and cos >= MIN_COS
+
+
 # full-size configurations against the fp32 reference on the GPU
 FULL = {
     "cfg2": dict(batch_size=4, num_heads=32, seq_len=4096, head_dim=128, k_offset_std=2.0, pv_dtype="fp16"),
