@@ -102,6 +102,37 @@ def test_attn_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
     assert torch.equal(o1, o2.transpose(1, 2))
 
 
+@pytest.mark.parametrize("sm_scale", [0.05, 0.3])
+def test_attn_explicit_sm_scale(sm_scale, pack_ref, hip_impl, gpu_device):
+    """run(..., sm_scale=s) (triton_impl.py:162, 60-61) against SDPA at the same scale."""
+    print(f"[attn-sm_scale] {sm_scale}", flush=True)
+    inp = pack_ref.make_inputs(dict(batch_size=1, num_heads=4, num_kv_heads=2, seq_len=700, head_dim=128,
+                                    k_offset_std=2.0), "cpu", 3, torch.bfloat16)
+    q, k, v = (inp[x].to(gpu_device) for x in ("q", "k", "v"))
+    o, pre = hip_impl.run(q, k, v, sm_scale=sm_scale, return_intermediates=True)
+    torch.cuda.synchronize()
+    got = o.float().cpu().numpy()
+    qf, kf, vf = (inp[x].float().numpy() for x in ("q", "k", "v"))
+    want = O.sdpa(qf, kf, vf, sm_scale=sm_scale)
+    emu = O.sage_emulate(pre["q8"].cpu().numpy(), pre["q_scale"].cpu().numpy(), pre["k8"].cpu().numpy(),
+                         pre["k_scale"].cpu().numpy(), vf)
+    assert np.array_equal(pre["q_scale"].cpu().numpy(),
+                          O.quant_per_block_int8(qf, 128, mul=O.q_multiplier(128, sm_scale))[1])
+    max_abs, cos = _metrics(got, want)
+    quant_err, quant_cos = _metrics(emu, want)
+    print(f"  kernel vs fp64 SDPA: max_abs={max_abs:.3e} cos={cos:.6f} "
+          f"(emulation vs SDPA: {quant_err:.3e}, cos {quant_cos:.6f})")
+    assert _vs_emulation(got, emu, torch.bfloat16) <= EMUL_ABS
+    # A larger scale sharpens the softmax and with it the INT8 error of the
+    # scores themselves (the exact emulation has it too): the SDPA gate then
+    # becomes "no worse than the quantization".
+    slack = EMUL_ABS + OUT_EPS[torch.bfloat16] * float(np.abs(emu).max())
+    assert max_abs <= max(MAX_ABS, quant_err + slack)
+    assert cos >= min(MIN_COS, quant_cos - 1e-4)
+    if sm_scale <= 0.1:
+        assert max_abs <= MAX_ABS and cos >= MIN_COS
+
+
 # Nq != Nkv (the reference's per_block_int8 takes them separately, triton_impl.py:43-44):
 # cross attention and a decode-like single query row; causal is top-left
 # (key j visible to query i iff j <= i), so rows >= Nkv see every key.

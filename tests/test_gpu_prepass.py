@@ -103,6 +103,21 @@ def test_per_block_int8_mirror(pack_ref, hip_impl, gpu_device):
     assert np.array_equal(k8.cpu().numpy(), wk8) and np.array_equal(ks.cpu().numpy(), wks)
 
 
+def test_per_block_int8_sm_scale_and_block_sizes(pack_ref, hip_impl, gpu_device):
+    """Explicit sm_scale (triton_impl.py:60-61, 69) and non-default BLKQ / BLKK
+    (the function's arguments, triton_impl.py:35), NHD layout: bit-exact."""
+    inp = _inputs(pack_ref, 2, 4, 2, 300, 64, "bf16", 2.0, "normal")
+    q, k = inp["q"].to(gpu_device), inp["k"].to(gpu_device)
+    qn, kn = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    q8, qs, k8, ks = hip_impl.per_block_int8(qn, kn, BLKQ=64, BLKK=128, sm_scale=0.0371, tensor_layout="NHD")
+    torch.cuda.synchronize()
+    assert q8.shape == qn.shape and qs.shape == (2, 4, 5) and ks.shape == (2, 2, 3)
+    wq8, wqs = O.quant_per_block_int8(_np32(q), 64, mul=O.q_multiplier(64, 0.0371))
+    wk8, wks = O.quant_per_block_int8(_np32(k), 128)
+    assert np.array_equal(q8.transpose(1, 2).cpu().numpy(), wq8) and np.array_equal(qs.cpu().numpy(), wqs)
+    assert np.array_equal(k8.transpose(1, 2).cpu().numpy(), wk8) and np.array_equal(ks.cpu().numpy(), wks)
+
+
 def test_prepass_special_blocks(hip_impl, gpu_device):
     """All-zero block, exact ties, the 0x3EFFFFFF quirk, -0.0, tiny values."""
     D = 64
