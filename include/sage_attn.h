@@ -13,6 +13,12 @@
  *   sage_attn_fwd() <- _attn_fwd[grid](...) launch    triton_impl.py:186-199
  *                      _attn_fwd / _attn_fwd_inner    triton_impl.py:86-160
  *
+ * and, with the same attention kernel on unquantized fp16/bf16 Q and K,
+ * the flash_attn pack's forward:
+ *
+ *   sage_flash_fwd() <- run_flash_attn / _flash_attn_fwd_kernel
+ *                       kernels/flash_attn/triton_impl.py:12-121
+ *
  * The Python entry point that strings them together (the counterpart of
  * run_sage_attn, triton_impl.py:162-200) lives in
  * tribench_amd/kernels/sage_attn/hip_impl.py and binds this header with ctypes.
@@ -41,7 +47,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 2
+#define SAGE_ABI_VERSION 3
 
 /* element types (dtype codes used by every entry point) */
 #define SAGE_DTYPE_F32 0
@@ -143,6 +149,25 @@ int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_sc
                   void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
                   int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq, int blkk,
                   int q_sub, int pv_mode, void* stream);
+
+/*
+ * Unquantized attention: S = Q K^T from fp16/bf16 MFMAs (fp32 accumulate),
+ * the online base-2 softmax of sage_attn_fwd, P rounded to the input type
+ * (the reference casts p to V's dtype, kernels/flash_attn/triton_impl.py:87-88),
+ * O += P V in fp32.  Replaces run_flash_attn (kernels/flash_attn/triton_impl.py:103-121).
+ *
+ *  q [B,Hq,Nq,D], k [B,Hkv,Nkv,D]  in_dtype (F16 or BF16), strides as above
+ *  v       the V tiles of sage_vtiles() with pv_mode SAGE_PV_F16 for fp16
+ *          inputs, SAGE_PV_BF16 for bf16 (v_dtype SAGE_DTYPE_VTILES;
+ *          v_strides is not read and may be NULL)
+ *  o       [B,Hq,Nq,D] in in_dtype
+ *  qk_mul  fp32(sm_scale * 1.44269504): the scores in log2 units
+ *  causal and GQA as in sage_attn_fwd.
+ */
+int sage_flash_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                   const void* v, int v_dtype, const int64_t* v_strides, void* o, const int64_t* o_strides,
+                   int in_dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                   float qk_mul, int causal, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,8 +24,9 @@ def lib(hip_impl):
 
 
 def test_header_declares_the_entry_points():
-    assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_last_error", "sage_prepass",
-                                     "sage_prepass_workspace_bytes", "sage_vtile_bytes", "sage_vtiles"]
+    assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_flash_fwd", "sage_last_error",
+                                     "sage_prepass", "sage_prepass_workspace_bytes", "sage_vtile_bytes",
+                                     "sage_vtiles"]
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -110,3 +111,20 @@ def test_hip_variant_refuses_cpu_tensors(hip_impl):
     q = torch.zeros(1, 2, 16, 64)
     with pytest.raises(RuntimeError, match="ROCm GPU device"):
         hip_impl.run(q, q, q)
+
+
+def test_flash_rejects_bad_arguments(lib):
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    p = ctypes.c_void_p(16)
+    for args, needle in [
+        ((p, s3, p, s3, p, 4, None, p, s3, 1, 1, 2, 2, 64, 64, 96, 0.18, 0, None), "head_dim"),
+        ((p, s3, p, s3, p, 4, None, p, s3, 0, 1, 2, 2, 64, 64, 64, 0.18, 0, None), "in_dtype"),
+        ((p, s3, p, s3, p, 2, None, p, s3, 2, 1, 2, 2, 64, 64, 64, 0.18, 0, None), "v_dtype"),
+        ((p, s3, p, s3, p, 4, None, p, s3, 2, 1, 3, 2, 64, 64, 64, 0.18, 0, None), "Hq"),
+        ((p, s3, p, s3, p, 4, None, p, s3, 2, 1, 2, 2, 64, 64, 64, 0.0, 0, None), "qk_mul"),
+        ((None, s3, p, s3, p, 4, None, p, s3, 2, 1, 2, 2, 64, 64, 64, 0.18, 0, None), "null"),
+        ((ctypes.c_void_p(8), s3, p, s3, p, 4, None, p, s3, 2, 1, 2, 2, 64, 64, 64, 0.18, 0, None), "aligned"),
+    ]:
+        rc = lib.sage_flash_fwd(*args)
+        msg = lib.sage_last_error().decode()
+        assert rc != 0 and "invalid argument" in msg and needle in msg, msg

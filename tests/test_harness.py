@@ -95,6 +95,35 @@ def test_sage_pack_meta_and_entrypoints():
     assert {"s4k_d64", "s8k_d64", "cfg1_b1h2n256d64", "cfg2_b4h32n4096d128"} <= set(names)
 
 
+def test_flash_pack_meta_entrypoints_and_shared_reference():
+    """The flash_attn pack (kernels/flash_attn/meta.json of the reference, plus a
+    hip variant): valid meta, the reference's two cases, and make_inputs / ref /
+    estimate that agree with the sage_attn pack and the oracle."""
+    import numpy as np
+    import torch
+
+    from oracle import sage_oracle as O
+
+    reg = KernelRegistry()
+    meta = reg.get_meta("flash_attn")
+    assert meta.entrypoints.variants == {"hip": "hip_impl.py:run"}
+    assert validate_entrypoints(meta) == []
+    assert {"s4k_d64", "s8k_d64"} <= {c.name for c in meta.cases}
+    ref_mod = reg.load_symbol("flash_attn", "reference.py:ref").__module__
+    assert ref_mod == "tribench.kernels.flash_attn.reference"
+    make = reg.load_symbol("flash_attn", "reference.py:make_inputs")
+    ref = reg.load_symbol("flash_attn", "reference.py:ref")
+    est = reg.load_symbol("flash_attn", "reference.py:estimate")
+    case = dict(batch_size=1, num_heads=2, seq_len=70, head_dim=64, causal=True)
+    inp = make(case, "cpu", 0, torch.float16)
+    assert inp["q"].dtype == torch.float16 and inp["q"].shape == (1, 2, 70, 64) and inp["causal"]
+    out = ref(inp["q"], inp["k"], inp["v"], causal=True)
+    want = O.sdpa(inp["q"].float().numpy(), inp["k"].float().numpy(), inp["v"].float().numpy(), causal=True)
+    assert np.abs(out.numpy() - want).max() < 1e-5
+    e = est(dict(batch_size=8, num_heads=16, seq_len=4096, head_dim=64))
+    assert e["flops"] == 4 * 8 * 16 * 4096 * 4096 * 64 and e["bytes"] == 4 * 8 * 16 * 4096 * 64 * 2
+
+
 # ---------------------------------------------------------------------------
 # registry / case grid / inputs / reference / estimate
 # ---------------------------------------------------------------------------
@@ -275,3 +304,12 @@ def test_load_meta_keeps_case_params():
     meta = load_meta(Path(KernelRegistry().get_meta("sage_attn").kernel_dir) / "meta.json")
     c = {x.name: x.params for x in meta.cases}["cfg5_fp8pv_b1h32n32768d128"]
     assert c["pv_dtype"] == "fp8" and c["q_gran"] == "wave" and "name" not in c
+
+
+def test_roofline_unit_per_pack():
+    from tribench_amd.harness.cli import roofline_unit_for
+
+    reg = KernelRegistry()
+    assert roofline_unit_for(reg.get_meta("sage_attn"), {"dtype": "bf16"}) == "int8"
+    assert roofline_unit_for(reg.get_meta("flash_attn"), {"dtype": "fp16"}) == "fp16"
+    assert roofline_unit_for(reg.get_meta("flash_attn"), {"dtype": "bf16"}) == "bf16"

@@ -1,7 +1,10 @@
 // sage_attn_fwd.hip — fused SageAttention forward for gfx950 (MI355X).
 //
 // Replaces _attn_fwd / _attn_fwd_inner (kernels/sage_attn/triton_impl.py:86-160)
-// and its launch (:186-199).  Per block of 64 keys:
+// and its launch (:186-199); with fp16/bf16 Q and K instead of INT8 (no
+// quantization, S in fp32 from v_mfma_f32_32x32x16_{f16,bf16}) the same
+// kernel replaces _flash_attn_fwd_kernel (kernels/flash_attn/triton_impl.py:
+// 12-101).  Per block of 64 keys:
 //   S^T = K8 . Q8^T          v_mfma_i32_32x32x32_i8 (INT8, i32 accumulate)
 //   s   = float(S) * (q_scale * k_scale)          (triton_impl.py:99)
 //   online base-2 softmax: m, l, p = exp2(s - m)   (triton_impl.py:102-109)
@@ -41,6 +44,8 @@
 //  * Work-group ids are remapped so that all q-blocks of one (batch, head)
 //    run on one XCD (shared L2): the hardware deals work-groups to the 8 XCDs
 //    round-robin.
+#include <type_traits>
+
 #include "sage_device.h"
 
 namespace sage {
@@ -50,9 +55,9 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 
 struct AttnArgs {
-  const int8_t* q8;
+  const void* q8;         // INT8 Q (or fp16/bf16 Q of the unquantized kernel)
   const float* q_scale;
-  const int8_t* k8;
+  const void* k8;         // INT8 K (or fp16/bf16 K)
   const float* k_scale;
   const void* v;          // V tiles (sage_vtiles layout)
   const float* v_scale;
@@ -63,7 +68,12 @@ struct AttnArgs {
   int causal;
   int q_sub, blkk_shift;  // k scale of key block j: k_scale[j >> blkk_shift]
   int nqs, nks;           // q / k scales per head
+  float qk_mul;           // unquantized kernel: score multiplier, fp32(sm_scale * log2(e))
 };
+
+// Operand type of the QK product: INT8 with per-block scales (SageAttention)
+// or fp16 / bf16 (plain attention, no scales).
+constexpr int kQkI8 = 0, kQkF16 = 1, kQkBF16 = 2;
 
 constexpr int kBN = 64;  // keys per block
 
@@ -158,6 +168,10 @@ __device__ __forceinline__ int max_halves(int v) {
   const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
   return max((int)a[0], (int)a[1]);
 }
+__device__ __forceinline__ float max_halves_f(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float((int)a[0]), __int_as_float((int)a[1]));
+}
 __device__ __forceinline__ float sum_halves(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
   return __int_as_float((int)a[0]) + __int_as_float((int)a[1]);
@@ -188,22 +202,25 @@ typedef __attribute__((address_space(1))) const void gmem_t;
 typedef __attribute__((address_space(3))) void lmem_t;
 
 // One work-group: 8 waves (2 per SIMD) of 32 query rows (one 32-row MFMA tile
-// each) of one (batch, head); Q8 rows, S, P and the O^T accumulators live in
-// arch VGPRs.  Tiles of 64 keys (K8 rows and V^T rows) reach LDS by direct
+// each) of one (batch, head); Q rows, S, P and the O^T accumulators live in
+// arch VGPRs.  Tiles of 64 keys (K rows and V^T rows) reach LDS by direct
 // global -> LDS loads, three tiles ahead of their use, in a ring of 5.
-template <int D, int PVM, typename TO>
+template <int QKM, int D, int PVM, typename TO>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BM = 256;  // query rows per work-group
+  constexpr bool kI8 = QKM == kQkI8;
   constexpr bool kF8 = PVM == SAGE_PV_FP8;
   using Pv = PvT<PVM>;
+  using SAcc = std::conditional_t<kI8, v16i, v16f>;  // S^T accumulator of one 32-key tile
+  constexpr int QEB = kI8 ? 1 : 2;  // bytes per Q / K element
   constexpr int EB = Pv::kEB;
-  constexpr int KC = D / 32;        // 32-byte slices of the QK contraction
+  constexpr int KRB = D * QEB;      // K row bytes
+  constexpr int KC = KRB / 32;      // 32-byte slices of a K row: one QK MFMA each
   constexpr int DT = D / 32;        // 32-row d tiles of O^T
   constexpr int PW = Pv::kPW;       // P dwords per lane
-  constexpr int KRB = D;            // K8 row bytes
   constexpr int VRB = 64 * EB;      // V^T row bytes
-  constexpr int KTB = kBN * KRB;    // K8 tile bytes
+  constexpr int KTB = kBN * KRB;    // K tile bytes
   constexpr int VTB = D * VRB;      // V^T tile bytes
   constexpr int SLOT = KTB + VTB;
   constexpr int NBUF = 5;           // tiles j-1 .. j+3 of iteration j
@@ -211,8 +228,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int VLD = VTB / 1024;
   constexpr int LPW = (KLD + VLD + NW - 1) / NW;  // wave loads per wave per tile
   static_assert(LPW * NW >= KLD + VLD && LPW <= 15, "tile loads");
+  constexpr int SINK = LPW * NW > KLD + VLD ? 1024 : 0;  // target of spare loads
 
-  __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT + 1024];  // + a sink for spare loads
+  __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT + SINK];
 
   const int nqb = (a.Nq + BM - 1) / BM;
   const int wg = remap_xcd((int)blockIdx.x, (int)gridDim.x);
@@ -229,8 +247,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int q0 = qb * BM;
   const int qa = q0 + wave * 32;  // first q row of this wave
 
-  const int8_t* qbase = a.q8 + b * a.sq[0] + h * a.sq[1];
-  const int8_t* kbase = a.k8 + b * a.sk[0] + hk * a.sk[1];
+  const char* qbase = static_cast<const char*>(a.q8) + (b * a.sq[0] + h * a.sq[1]) * QEB;
+  const char* kbase = static_cast<const char*>(a.k8) + (b * a.sk[0] + hk * a.sk[1]) * QEB;
   // k scales are read through the constant address space (scalar loads, which
   // the tile-load accounting on vmcnt does not see); the kernel never writes them
   typedef __attribute__((address_space(4))) const float cfloat_t;
@@ -238,16 +256,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ntile = (a.Nkv + kBN - 1) / kBN;
   const uint8_t* vtbase = static_cast<const uint8_t*>(a.v) + ((int64_t)b * a.Hkv + hk) * ntile * (int64_t)VTB;
 
-  // ---- Q8, the B operand of S^T = K Q^T: row qa + n, bytes 32c + 16hh .. +16.
+  // ---- Q, the B operand of S^T = K Q^T: row qa + n, bytes 32c + 16hh .. +16.
   // Rows past Nq read the last row; their results are never stored.
   v4i qreg[KC];
   {
     const int row = min(qa + n, a.Nq - 1);
 #pragma unroll
     for (int c = 0; c < KC; ++c)
-      qreg[c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn + 32 * c + 16 * hh));
+      qreg[c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn * QEB + 32 * c + 16 * hh));
   }
-  const float qsc = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)];
+  const float qsc = kI8 ? a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)] : 1.0f;
 
   // ---- key blocks of the work-group and of this wave
   const int nkb_all = ntile;
@@ -282,14 +300,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const int p = 64 * g + lane;
         const int r = p / (KRB / 16), pc = p % (KRB / 16);
         const int row = min(k0 + r, a.Nkv - 1);
-        src = kbase + (uint32_t)(row * a.skn + 16 * (pc ^ swz<KRB>(r)));
+        src = kbase + (uint32_t)(row * a.skn * QEB + 16 * (pc ^ swz<KRB>(r)));
         dst = slot + 1024 * g;
       } else if (g < KLD + VLD) {
         const int p = 64 * (g - KLD) + lane;
         const int d = p / (VRB / 16), pc = p % (VRB / 16);
         src = vt + d * VRB + 16 * (pc ^ swz<VRB>(d));
         dst = slot + KTB + 1024 * (g - KLD);
-      } else {
+      } else {  // only when SINK > 0
         src = kbase;
         dst = smem + NBUF * SLOT;
       }
@@ -313,14 +331,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float lsum = 0.0f;     // this lane's share of the row sum
   float alpha_o = 1.0f;  // pending factor of O
   bool pend = false;     // O must be multiplied by alpha_o before the next P.V
-  v16i S[2];             // S^T of key tiles 0 and 1 of the block in flight
-  float ksc_cur = 0.0f;  // k scale of the block held in S
+  SAcc S[2];             // S^T of key tiles 0 and 1 of the block in flight
+  float ksc_cur = 0.0f;  // k scale of the block held in S (INT8)
   uint32_t Pprev[PW], Pcur[PW];  // P of blocks j-1 and j
   const v16i magic = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
                       kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
 
   // per-lane byte offsets of the swizzled operand chunks
-  int koff[KC];  // K8 row 32t + n (swizzle independent of t), logical chunk 2c + hh
+  int koff[KC];  // K row 32t + n (swizzle independent of t), logical chunk 2c + hh
 #pragma unroll
   for (int c = 0; c < KC; ++c) koff[c] = n * KRB + 16 * ((2 * c + hh) ^ swz<KRB>(n));
   constexpr int VCH = kF8 ? 2 : 4;  // chunks of a V^T operand read per d tile
@@ -329,18 +347,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int c = 0; c < VCH; ++c) voff[c] = KTB + n * VRB + 16 * ((VCH * hh + c) ^ swz<VRB>(n));
 
   // ---- building blocks
-  // S^T of block j (its K8 tile in slot j % NBUF): K row 32t + n, bytes 32c + 16hh
+  // S^T of block j (its K tile in slot j % NBUF): K row 32t + n, bytes 32c + 16hh
   auto qk = [&](int j) __attribute__((always_inline)) {
     const char* ks = smem + (j % NBUF) * SLOT;
-    ksc_cur = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
+    if constexpr (kI8) ksc_cur = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       v4i ka[KC];
 #pragma unroll
       for (int c = 0; c < KC; ++c) ka[c] = *reinterpret_cast<const v4i*>(ks + 32 * t * KRB + koff[c]);
 #pragma unroll
-      for (int c = 0; c < KC; ++c)
-        S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qreg[c], c == 0 ? magic : S[t], 0, 0, 0);
+      for (int c = 0; c < KC; ++c) {
+        if constexpr (kI8) {
+          S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qreg[c], c == 0 ? magic : S[t], 0, 0, 0);
+        } else if constexpr (QKM == kQkF16) {
+          S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ka[c]), __builtin_bit_cast(v8h, qreg[c]),
+                                                        c == 0 ? (v16f){} : S[t], 0, 0, 0);
+        } else {
+          S[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ka[c]),
+                                                         __builtin_bit_cast(v8bf, qreg[c]), c == 0 ? (v16f){} : S[t],
+                                                         0, 0, 0);
+        }
+      }
     }
   };
   // O^T += V^T P^T of block j (its V^T tile in slot j % NBUF)
@@ -374,24 +402,42 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   // softmax of block j held in S -> P (and the running max / sums).  Max and
   // sum are pairwise trees, not serial chains, to keep dependency depth low.
+  // c > 0 scales S to log2 units: q_scale * k_scale (INT8) or qk_mul.
   auto softmax = [&](int j, uint32_t (&P)[PW], bool masked) __attribute__((always_inline)) {
     const int k0 = j * kBN;
     const int qrow = qa + n;
-    const float c = qsc * ksc_cur;
-    int x[32];
+    const float c = kI8 ? qsc * ksc_cur : a.qk_mul;
+    float mblk;
+    if constexpr (kI8) {
+      int x[32];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        x[16 * t + v] = S[t][v];
-        if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = INT_MIN;
-      }
+        for (int v = 0; v < 16; ++v) {
+          x[16 * t + v] = S[t][v];
+          if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = INT_MIN;
+        }
 #pragma unroll
-    for (int w = 16; w >= 1; w >>= 1)
+      for (int w = 16; w >= 1; w >>= 1)
 #pragma unroll
-      for (int i = 0; i < w; ++i) x[i] = max(x[i], x[i + w]);
-    const int mx = max_halves(x[0]);
-    const float mblk = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * c;
+        for (int i = 0; i < w; ++i) x[i] = max(x[i], x[i + w]);
+      const int mx = max_halves(x[0]);
+      mblk = mx == INT_MIN ? -INFINITY : (float)(mx - kMagicI) * c;
+    } else {
+      float x[32];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          x[16 * t + v] = S[t][v];
+          if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = -INFINITY;
+        }
+#pragma unroll
+      for (int w = 16; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) x[i] = fmaxf(x[i], x[i + w]);
+      mblk = max_halves_f(x[0]) * c;
+    }
     // lazy max update (per q column; both lane halves agree)
     const bool need = mblk > m_use + SoftmaxCfg<PVM>::kTau;
     const float mnew = need ? mblk : m_use;
@@ -401,14 +447,16 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     alpha_o *= alpha;
     pend |= __builtin_amdgcn_ballot_w64(need) != 0;
     const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
-    const float bias = __builtin_fmaf(kMagicF, c, m);  // x = (2^23+2^22+S)*c - bias = S*c - m
+    // INT8: S reads as the float 2^23 + 2^22 + S, so S*c - m = that*c - bias
+    const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
     float ls[2];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float p[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        float e = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(S[t][v]), c, -bias));
+        const float sv = kI8 ? __int_as_float((int)S[t][v]) : (float)S[t][v];
+        float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, -bias));
         if (masked) e = key_ok(k0 + key_of(t, v), qrow) ? e : 0.0f;
         p[v] = e;
       }
@@ -511,18 +559,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
-template <int D, int PVM, typename TO>
-static int launch_cfg(const AttnArgs& a, hipStream_t st) {
+template <int QKM, int D, int PVM, typename TO>
+static int launch_cfg(const AttnArgs& a, hipStream_t st, const char* who) {
   const int64_t nqb = (a.Nq + 255) / 256;
   const int64_t grid = nqb * a.Hq * a.B;
-  if (grid > 0x7FFFFFFF) return fail("sage_attn_fwd: invalid argument: grid too large");
-  hipLaunchKernelGGL((attn_fwd_kernel<D, PVM, TO>), dim3((unsigned)grid), dim3(512), 0, st, a);
-  return check_launch("sage_attn_fwd");
+  if (grid > 0x7FFFFFFF) return fail("%s: invalid argument: grid too large", who);
+  hipLaunchKernelGGL((attn_fwd_kernel<QKM, D, PVM, TO>), dim3((unsigned)grid), dim3(512), 0, st, a);
+  return check_launch(who);
 }
 
 template <int PVM, typename TO>
 static int launch_d(const AttnArgs& a, int D, hipStream_t st) {
-  return D == 64 ? launch_cfg<64, PVM, TO>(a, st) : launch_cfg<128, PVM, TO>(a, st);
+  return D == 64 ? launch_cfg<kQkI8, 64, PVM, TO>(a, st, "sage_attn_fwd")
+                 : launch_cfg<kQkI8, 128, PVM, TO>(a, st, "sage_attn_fwd");
 }
 
 template <typename TO>
@@ -532,6 +581,15 @@ static int launch_pv(const AttnArgs& a, int D, int pv_mode, hipStream_t st) {
     case SAGE_PV_BF16: return launch_d<SAGE_PV_BF16, TO>(a, D, st);
     default: return launch_d<SAGE_PV_FP8, TO>(a, D, st);
   }
+}
+
+// unquantized kernel: QK in the input type, P.V in the input type (the
+// reference casts P to V's dtype, kernels/flash_attn/triton_impl.py:87-88)
+template <int QKM, typename TO>
+static int launch_flash(const AttnArgs& a, int D, hipStream_t st) {
+  constexpr int PVM = QKM == kQkF16 ? SAGE_PV_F16 : SAGE_PV_BF16;
+  return D == 64 ? launch_cfg<QKM, 64, PVM, TO>(a, st, "sage_flash_fwd")
+                 : launch_cfg<QKM, 128, PVM, TO>(a, st, "sage_flash_fwd");
 }
 
 static bool strides_ok(const int64_t* s, int esize) {
@@ -616,4 +674,59 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
     case SAGE_DTYPE_F16: return launch_pv<_Float16>(a, d, pv_mode, st);
     default: return launch_pv<__bf16>(a, d, pv_mode, st);
   }
+}
+
+extern "C" int sage_flash_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
+                              const void* v, int v_dtype, const int64_t* v_strides, void* o,
+                              const int64_t* o_strides, int in_dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                              int64_t Nq, int64_t Nkv, int64_t D, float qk_mul, int causal, void* stream) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0)
+    return fail("sage_flash_fwd: invalid argument: empty shape");
+  if (D != 64 && D != 128)
+    return fail("sage_flash_fwd: invalid argument: head_dim %lld (supported: 64, 128)", (long long)D);
+  if (Hq % Hkv != 0) return fail("sage_flash_fwd: invalid argument: Hq %% Hkv != 0");
+  if (Nq > 0x7FFFFFFF || Nkv > 0x7FFFFFFF || Hq > 0xFFFF || B > 0xFFFF)
+    return fail("sage_flash_fwd: invalid argument: shape too large");
+  if (in_dtype != SAGE_DTYPE_F16 && in_dtype != SAGE_DTYPE_BF16)
+    return fail("sage_flash_fwd: invalid argument: in_dtype %d (fp16 or bf16)", in_dtype);
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !o_strides)
+    return fail("sage_flash_fwd: invalid argument: null pointer");
+  if (v_dtype != SAGE_DTYPE_VTILES)
+    return fail("sage_flash_fwd: invalid argument: v_dtype %d (V must be in the tile layout of sage_vtiles)",
+                v_dtype);
+  if (!(qk_mul > 0.0f) || qk_mul == INFINITY) return fail("sage_flash_fwd: invalid argument: qk_mul %g", qk_mul);
+  const bool rows32 = (Nq * q_strides[2] + D) * 2 < 0x7FFFFFFF && (Nkv * k_strides[2] + D) * 2 < 0x7FFFFFFF &&
+                      Nq * o_strides[2] + D < 0x7FFFFFFF;
+  if (!rows32) return fail("sage_flash_fwd: invalid argument: a head's rows must span < 2^31 bytes");
+  if (!strides_ok(q_strides, 2) || !strides_ok(k_strides, 2) || !strides_ok(o_strides, 2))
+    return fail("sage_flash_fwd: invalid argument: strides must keep 16-byte aligned rows");
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)o) % 16 != 0)
+    return fail("sage_flash_fwd: invalid argument: base pointers must be 16-byte aligned");
+
+  AttnArgs a{};
+  a.q8 = q;
+  a.k8 = k;
+  a.v = v;
+  a.o = o;
+  for (int i = 0; i < 2; ++i) {
+    a.sq[i] = q_strides[i];
+    a.sk[i] = k_strides[i];
+    a.so[i] = o_strides[i];
+  }
+  a.sqn = (int)q_strides[2];
+  a.skn = (int)k_strides[2];
+  a.son = (int)o_strides[2];
+  a.B = (int)B;
+  a.Hq = (int)Hq;
+  a.Hkv = (int)Hkv;
+  a.Nq = (int)Nq;
+  a.Nkv = (int)Nkv;
+  a.causal = causal ? 1 : 0;
+  a.q_sub = 32;
+  a.nqs = a.nks = 1;
+  a.qk_mul = qk_mul;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int d = (int)D;
+  return in_dtype == SAGE_DTYPE_F16 ? launch_flash<kQkF16, _Float16>(a, d, st)
+                                    : launch_flash<kQkBF16, __bf16>(a, d, st);
 }

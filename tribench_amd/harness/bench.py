@@ -201,8 +201,11 @@ def run_benchmark(
         effective_tops=tflops,
         algo_tops=compute_tflops(algo, p50) if algo else None,
         roofline_peak=peak, roofline_unit=roofline_unit,
-        roofline_fraction=(tflops / peak) if (tflops and peak) else None,
     )
+    # the roofline counts the work done (unmasked pairs for causal cases),
+    # not the metric's 4*B*H*N^2*D
+    rate = res.algo_tops if res.algo_tops else tflops
+    res.roofline_fraction = (rate / peak) if (rate and peak) else None
     pre_fn = (stage_fns or {}).get("prepass")
     if pre_fn is not None and device.startswith("cuda"):
         pre_lats = timer(lambda: pre_fn(**inputs), warmup_ms / 4, rep_ms / 4)

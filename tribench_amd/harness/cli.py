@@ -56,6 +56,14 @@ def _first_line(e: Exception) -> str:
     return s.splitlines()[0] if s else ""
 
 
+def roofline_unit_for(meta, case) -> str:
+    """MFMA peak a case is priced against: INT8 for packs tagged "int8" (the
+    quantized QK product dominates), else the case's dtype."""
+    if "int8" in (getattr(meta, "tags", None) or []):
+        return "int8"
+    return case.get("dtype", "bf16") if case.get("dtype") in ("fp16", "bf16", "fp32") else "bf16"
+
+
 def _print_error(prefix: str, e: Exception) -> None:
     from .errors import get_hint
 
@@ -213,7 +221,8 @@ def _cmd_run(args) -> int:
                                         reference_fn=reference, triton_fn=fn, estimate_fn=estimate, case=case,
                                         device=args.device, seed=args.seed, warmup_ms=args.warmup_ms,
                                         rep_ms=args.rep_ms, quantiles=quantiles, timer_backend=args.timer,
-                                        run_correctness=not args.no_correctness, stage_fns=stages)
+                                        run_correctness=not args.no_correctness, stage_fns=stages,
+                                        roofline_unit=roofline_unit_for(meta, case))
                 except Exception as e:
                     failed = True
                     print(f"    SKIP  {case['case_name']} [{impl_name}] dtype={case['dtype']}  (benchmark exception)")

@@ -26,7 +26,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
 
@@ -83,6 +83,9 @@ def _load():
         vp, p64, vp, vp, p64, vp, vp, i32, p64, vp, vp, i32, p64, i64, i64, i64, i64, i64, i64, i32,
         i32, i32, i32, i32, vp,
     ]
+    lib.sage_flash_fwd.restype = i32
+    lib.sage_flash_fwd.argtypes = [vp, p64, vp, p64, vp, i32, p64, vp, p64, i32, i64, i64, i64, i64, i64, i64, f32,
+                                   i32, vp]
     ver = lib.sage_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"sage_attn hip: library ABI {ver}, expected {ABI_VERSION}")
