@@ -47,7 +47,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 3
+#define SAGE_ABI_VERSION 4
 
 /* element types (dtype codes used by every entry point) */
 #define SAGE_DTYPE_F32 0
@@ -101,6 +101,8 @@ size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t
  *            v_scale only (v_mode FP8_SCALE; v8 may be NULL)
  *  q8/k8/v8 strides are given like the input strides; scales, km and
  *  v_scale are dense.
+ *  q, q_strides, q8, q8_strides and q_scale may all be NULL: K (and V) only,
+ *  for sage_attn_fwd_q, which quantizes Q itself.
  */
 int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int64_t B, int64_t Hq,
                  int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, const int64_t* q_strides,
@@ -149,6 +151,25 @@ int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_sc
                   void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
                   int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq, int blkk,
                   int q_sub, int pv_mode, void* stream);
+
+/*
+ * sage_attn_fwd with the Q quantization of sage_prepass done in the kernel's
+ * prologue (fused, so Q is read once and Q8 never reaches memory): the
+ * per-block INT8 quantization of per_block_int8 (triton_impl.py:25-33, 63-71)
+ * with the same arithmetic, hence the same Q8 and q_scale bit for bit.
+ *
+ *  q [B,Hq,Nq,D] in q_dtype (F32/F16/BF16); o has q's type, o_strides its own
+ *  q_mul     fp32(sm_scale * 1.44269504), as for sage_prepass
+ *  blkq      must be 128 (four 32-row waves); q_sub 32, 64 or 128
+ *  q8_out, q_scale_out  optional (NULL: not written): Q8 with q's element
+ *            strides and q_scale [B,Hq,ceil(Nq/128)*(128/q_sub)]
+ *  everything else as sage_attn_fwd.
+ */
+int sage_attn_fwd_q(const void* q, const int64_t* q_strides, int q_dtype, float q_mul, int8_t* q8_out,
+                    float* q_scale_out, const int8_t* k8, const int64_t* k8_strides, const float* k_scale,
+                    const void* v, int v_dtype, const int64_t* v_strides, const float* v_scale, void* o,
+                    const int64_t* o_strides, int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv,
+                    int64_t D, int causal, int blkq, int blkk, int q_sub, int pv_mode, void* stream);
 
 /*
  * Unquantized attention: S = Q K^T from fp16/bf16 MFMAs (fp32 accumulate),

@@ -24,9 +24,9 @@ def lib(hip_impl):
 
 
 def test_header_declares_the_entry_points():
-    assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_flash_fwd", "sage_last_error",
-                                     "sage_prepass", "sage_prepass_workspace_bytes", "sage_vtile_bytes",
-                                     "sage_vtiles"]
+    assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_attn_fwd_q", "sage_flash_fwd",
+                                     "sage_last_error", "sage_prepass", "sage_prepass_workspace_bytes",
+                                     "sage_vtile_bytes", "sage_vtiles"]
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -67,6 +67,7 @@ def _prepass_args(**over):
     (dict(smooth=1), "km is null"),
     (dict(q=None), "null pointer"),
     (dict(q=ctypes.c_void_p(8)), "aligned"),
+    (dict(q=None, qs=None, q8s=None, qsc=None), "null pointer"),  # q8 given without q
 ])
 def test_prepass_rejects_bad_arguments(lib, over, needle):
     rc = lib.sage_prepass(*_prepass_args(**over))
@@ -126,5 +127,28 @@ def test_flash_rejects_bad_arguments(lib):
         ((ctypes.c_void_p(8), s3, p, s3, p, 4, None, p, s3, 2, 1, 2, 2, 64, 64, 64, 0.18, 0, None), "aligned"),
     ]:
         rc = lib.sage_flash_fwd(*args)
+        msg = lib.sage_last_error().decode()
+        assert rc != 0 and "invalid argument" in msg and needle in msg, msg
+
+
+def test_attn_fwd_q_rejects_bad_arguments(lib):
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    p = ctypes.c_void_p(16)
+    base = dict(q=p, qs=s3, qdt=2, qmul=0.18, q8o=None, qso=None, k8=p, k8s=s3, ksc=p, v=p, vdt=4, vs=None,
+                vsc=None, o=p, os=s3, B=1, Hq=2, Hkv=2, Nq=64, Nkv=64, D=64, causal=0, blkq=128, blkk=64,
+                q_sub=128, pv=0, st=None)
+    for over, needle in [
+        (dict(blkq=64, q_sub=64), "blkq"),
+        (dict(q_sub=48), "q_sub"),
+        (dict(qdt=9), "q_dtype"),
+        (dict(qmul=-1.0), "q_mul"),
+        (dict(vdt=2), "v_dtype"),
+        (dict(q=None), "null"),
+        (dict(D=96), "head_dim"),
+        (dict(q8o=ctypes.c_void_p(8)), "aligned"),
+    ]:
+        a = dict(base)
+        a.update(over)
+        rc = lib.sage_attn_fwd_q(*a.values())
         msg = lib.sage_last_error().decode()
         assert rc != 0 and "invalid argument" in msg and needle in msg, msg

@@ -102,6 +102,39 @@ def test_attn_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
     assert torch.equal(o1, o2.transpose(1, 2))
 
 
+# Q quantized in the attention kernel's prologue (sage_attn_fwd_q, run's default)
+# against the pre-pass path: the same Q8 and scales bit for bit (and the
+# oracle's), hence the same output bit for bit.
+# (B, Hq, Hkv, N, D, dtype, causal, q_gran, layout)
+FUSED = [
+    (2, 4, 2, 300, 128, "bf16", True, "block", "HND"),
+    (1, 3, 3, 1000, 64, "fp16", False, "wave", "HND"),
+    (1, 2, 2, 777, 128, "fp32", False, "block", "NHD"),
+    (1, 6, 1, 129, 64, "bf16", True, "wave", "NHD"),
+]
+
+
+@pytest.mark.parametrize("case", FUSED, ids=lambda c: f"B{c[0]}Hq{c[1]}Hkv{c[2]}N{c[3]}D{c[4]}-{c[5]}-c{int(c[6])}-{c[7]}-{c[8]}")
+def test_fused_q_matches_prepass(case, pack_ref, hip_impl, gpu_device):
+    B, Hq, Hkv, N, D, dtype, causal, q_gran, layout = case
+    print(f"[attn-fused-q] {case}", flush=True)
+    inp = pack_ref.make_inputs(dict(batch_size=B, num_heads=Hq, num_kv_heads=Hkv, seq_len=N, head_dim=D,
+                                    k_offset_std=2.0), "cpu", 7, DT[dtype])
+    q, k, v = (inp[x].to(gpu_device) for x in ("q", "k", "v"))
+    if layout == "NHD":
+        q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    kw = dict(causal=causal, q_gran=q_gran, tensor_layout=layout, return_intermediates=True)
+    o1, pre1 = hip_impl.run(q, k, v, fuse_q=True, **kw)
+    o2, pre2 = hip_impl.run(q, k, v, fuse_q=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(pre1["q8"], pre2["q8"]) and torch.equal(pre1["q_scale"], pre2["q_scale"])
+    assert torch.equal(o1, o2)
+    q_sub = hip_impl.WAVE_ROWS if q_gran == "wave" else 128
+    wq8, wqs = O.quant_per_block_int8(inp["q"].float().numpy(), 128, mul=O.q_multiplier(D), q_sub=q_sub)
+    got_q8 = pre1["q8"].transpose(1, 2) if layout == "NHD" else pre1["q8"]
+    assert np.array_equal(got_q8.cpu().numpy(), wq8) and np.array_equal(pre1["q_scale"].cpu().numpy(), wqs)
+
+
 @pytest.mark.parametrize("sm_scale", [0.05, 0.3])
 def test_attn_explicit_sm_scale(sm_scale, pack_ref, hip_impl, gpu_device):
     """run(..., sm_scale=s) (triton_impl.py:162, 60-61) against SDPA at the same scale."""

@@ -69,11 +69,15 @@ struct AttnArgs {
   int q_sub, blkk_shift;  // k scale of key block j: k_scale[j >> blkk_shift]
   int nqs, nks;           // q / k scales per head
   float qk_mul;           // unquantized kernel: score multiplier, fp32(sm_scale * log2(e))
+  float q_mul;            // Q quantized here: its multiplier, fp32(sm_scale * 1.44269504)
+  int8_t* q8_out;         // Q quantized here: optional copies of Q8 (q's strides) and q_scale
+  float* qs_out;
 };
 
-// Operand type of the QK product: INT8 with per-block scales (SageAttention)
-// or fp16 / bf16 (plain attention, no scales).
-constexpr int kQkI8 = 0, kQkF16 = 1, kQkBF16 = 2;
+// Operand type of the QK product: INT8 with per-block scales (SageAttention;
+// Q quantized by the pre-pass, or here from Q in the output type), or
+// fp16 / bf16 (plain attention, no scales).
+constexpr int kQkI8 = 0, kQkF16 = 1, kQkBF16 = 2, kQkI8Q = 3;
 
 constexpr int kBN = 64;  // keys per block
 
@@ -209,11 +213,12 @@ template <int QKM, int D, int PVM, typename TO>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = 8;
   constexpr int BM = 256;  // query rows per work-group
-  constexpr bool kI8 = QKM == kQkI8;
+  constexpr bool kFQ = QKM == kQkI8Q;  // Q quantized in the prologue
+  constexpr bool kI8 = QKM == kQkI8 || kFQ;
   constexpr bool kF8 = PVM == SAGE_PV_FP8;
   using Pv = PvT<PVM>;
   using SAcc = std::conditional_t<kI8, v16i, v16f>;  // S^T accumulator of one 32-key tile
-  constexpr int QEB = kI8 ? 1 : 2;  // bytes per Q / K element
+  constexpr int QEB = kI8 ? 1 : 2;  // bytes per Q8 / K element in the QK operands
   constexpr int EB = Pv::kEB;
   constexpr int KRB = D * QEB;      // K row bytes
   constexpr int KC = KRB / 32;      // 32-byte slices of a K row: one QK MFMA each
@@ -247,7 +252,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int q0 = qb * BM;
   const int qa = q0 + wave * 32;  // first q row of this wave
 
-  const char* qbase = static_cast<const char*>(a.q8) + (b * a.sq[0] + h * a.sq[1]) * QEB;
+  const char* qbase = static_cast<const char*>(a.q8) + (b * a.sq[0] + h * a.sq[1]) * (kFQ ? (int)sizeof(TO) : QEB);
   const char* kbase = static_cast<const char*>(a.k8) + (b * a.sk[0] + hk * a.sk[1]) * QEB;
   // k scales are read through the constant address space (scalar loads, which
   // the tile-load accounting on vmcnt does not see); the kernel never writes them
@@ -259,13 +264,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // ---- Q, the B operand of S^T = K Q^T: row qa + n, bytes 32c + 16hh .. +16.
   // Rows past Nq read the last row; their results are never stored.
   v4i qreg[KC];
-  {
+  float qsc = 1.0f;
+  if constexpr (!kFQ) {
     const int row = min(qa + n, a.Nq - 1);
 #pragma unroll
     for (int c = 0; c < KC; ++c)
       qreg[c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn * QEB + 32 * c + 16 * hh));
+    if constexpr (kI8) qsc = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)];
   }
-  const float qsc = kI8 ? a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)] : 1.0f;
+  // Q quantized here (kFQ): its raw rows are requested now, the quantization
+  // runs in the prologue once the first tiles are requested too, so the Q
+  // load latency overlaps theirs.  Lane (n, hh) holds elements 32c + 16hh ..
+  // +16 of row qa + n, exactly the bytes of its Q8 operand.
+  Raw8<TO> qraw[kFQ ? KC : 1][2];
+  if constexpr (kFQ) {
+    const TO* qr = reinterpret_cast<const TO*>(qbase) + (int64_t)min(qa + n, a.Nq - 1) * a.sqn;
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+      qraw[c][0] = load8<TO>(qr + 32 * c + 16 * hh);
+      qraw[c][1] = load8<TO>(qr + 32 * c + 16 * hh + 8);
+    }
+  }
 
   // ---- key blocks of the work-group and of this wave
   const int nkb_all = ntile;
@@ -522,10 +541,62 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sync_tiles(true);
   };
 
-  // ---- prologue: tiles 0, 1, 2 requested, 0 and 1 awaited; S of block 0
+  // Q quantization (kFQ) with the pre-pass's arithmetic (per_block_int8,
+  // triton_impl.py:25-33, 69): x = fp32(q) * q_mul, scale = max|x| / 127 over
+  // the q_sub rows of the scale (rows past Nq left out), q8 =
+  // round-half-away(x / scale).  Waves of one scale meet through LDS and a
+  // barrier without a memory fence (the tile loads stay in flight).
+  auto quantize_q = [&]() __attribute__((always_inline)) {
+    if constexpr (kFQ) {
+#pragma clang fp contract(off)
+      __shared__ float qamax_s[NW];
+      const int row = qa + n;
+      const bool valid = row < a.Nq;
+      float xq[KC][16];
+      float am = 0.0f;
+#pragma unroll
+      for (int c = 0; c < KC; ++c)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          xq[c][e] = elem<TO>(qraw[c][e >> 3], e & 7) * a.q_mul;
+          am = fmaxf(am, fabsf(xq[c][e]));
+        }
+      am = __uint_as_float(wave_max_u32(__float_as_uint(valid ? am : 0.0f)));  // the wave's 32 rows
+      if (a.q_sub > 32) {  // a scale spans q_sub / 32 waves
+        if (lane == 0) qamax_s[wave] = am;
+        SAGE_WAIT_LGKM0();
+        wg_barrier();
+        const int per = a.q_sub / 32, w0 = wave / per * per;
+        for (int w = w0; w < w0 + per; ++w) am = fmaxf(am, qamax_s[w]);
+      }
+      qsc = block_scale(am);
+      const float rc = qsc > 0.0f ? 1.0f / qsc : 0.0f;
+      const bool fast = fast_div_ok(qsc);
+#pragma unroll
+      for (int c = 0; c < KC; ++c) {
+        int w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          w[e >> 2] |= (int)(uint32_t)(uint8_t)quant_elem(xq[c][e], qsc, rc, fast) << (8 * (e & 3));
+        qreg[c] = (v4i){w[0], w[1], w[2], w[3]};
+        if (a.q8_out && valid)
+          *reinterpret_cast<v4i*>(a.q8_out + b * a.sq[0] + h * a.sq[1] + (int64_t)row * a.sqn + 32 * c + 16 * hh) =
+              qreg[c];
+      }
+      // every sub-block of the ceil(Nq/128) blocks, those with no rows too (scale 0)
+      if (a.qs_out && lane == 0 && qa < (a.Nq + 127) / 128 * 128 && qa % a.q_sub == 0)
+        a.qs_out[((int64_t)b * a.Hq + h) * a.nqs + qa / a.q_sub] = qsc;
+    }
+  };
+
+  // ---- prologue: tiles 0, 1, 2 requested, 0 and 1 awaited; S of block 0.
+  // With fewer than 3 tiles the last one is requested again (same data into
+  // its own slot), so the number of loads issued after Q's is fixed and Q can
+  // be waited for without draining the tile loads.
   load_tile(0);
-  if (nkb > 1) load_tile(1);
-  if (nkb > 2) load_tile(2);
+  load_tile(min(1, nkb - 1));
+  load_tile(min(2, nkb - 1));
+  quantize_q();
   sync_tiles(nkb > 2);
   if (jmax >= 0) qk(0);
 
@@ -574,12 +645,28 @@ static int launch_d(const AttnArgs& a, int D, hipStream_t st) {
                  : launch_cfg<kQkI8, 128, PVM, TO>(a, st, "sage_attn_fwd");
 }
 
+template <int QKM, int PVM, typename TO>
+static int launch_d(const AttnArgs& a, int D, hipStream_t st, const char* who) {
+  return D == 64 ? launch_cfg<QKM, 64, PVM, TO>(a, st, who) : launch_cfg<QKM, 128, PVM, TO>(a, st, who);
+}
+
 template <typename TO>
 static int launch_pv(const AttnArgs& a, int D, int pv_mode, hipStream_t st) {
   switch (pv_mode) {
     case SAGE_PV_F16: return launch_d<SAGE_PV_F16, TO>(a, D, st);
     case SAGE_PV_BF16: return launch_d<SAGE_PV_BF16, TO>(a, D, st);
     default: return launch_d<SAGE_PV_FP8, TO>(a, D, st);
+  }
+}
+
+// INT8 attention with Q quantized in the kernel (Q and O share their type)
+template <typename TO>
+static int launch_pv_q(const AttnArgs& a, int D, int pv_mode, hipStream_t st) {
+  const char* who = "sage_attn_fwd_q";
+  switch (pv_mode) {
+    case SAGE_PV_F16: return launch_d<kQkI8Q, SAGE_PV_F16, TO>(a, D, st, who);
+    case SAGE_PV_BF16: return launch_d<kQkI8Q, SAGE_PV_BF16, TO>(a, D, st, who);
+    default: return launch_d<kQkI8Q, SAGE_PV_FP8, TO>(a, D, st, who);
   }
 }
 
@@ -600,61 +687,48 @@ static bool strides_ok(const int64_t* s, int esize) {
 
 static bool is_float_code(int c) { return c == SAGE_DTYPE_F32 || c == SAGE_DTYPE_F16 || c == SAGE_DTYPE_BF16; }
 
-}  // namespace sage
-
-using namespace sage;
-
-extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_scale,
-                             const int8_t* k8, const int64_t* k8_strides, const float* k_scale,
-                             const void* v, int v_dtype, const int64_t* v_strides, const float* v_scale,
-                             void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
-                             int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq,
-                             int blkk, int q_sub, int pv_mode, void* stream) {
-  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0)
-    return fail("sage_attn_fwd: invalid argument: empty shape");
-  if (D != 64 && D != 128) return fail("sage_attn_fwd: invalid argument: head_dim %lld (supported: 64, 128)",
-                                       (long long)D);
-  if (Hq % Hkv != 0) return fail("sage_attn_fwd: invalid argument: Hq %% Hkv != 0");
+// Checks and fills everything of AttnArgs but the Q operand.
+static int attn_setup(AttnArgs& a, const char* who, const int64_t* q_strides, int q_es, const int8_t* k8,
+                      const int64_t* k8_strides, const float* k_scale, const void* v, int v_dtype,
+                      const float* v_scale, void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
+                      int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq, int blkk, int q_sub,
+                      int pv_mode) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0) return fail("%s: invalid argument: empty shape", who);
+  if (D != 64 && D != 128) return fail("%s: invalid argument: head_dim %lld (supported: 64, 128)", who, (long long)D);
+  if (Hq % Hkv != 0) return fail("%s: invalid argument: Hq %% Hkv != 0", who);
   if (Nq > 0x7FFFFFFF || Nkv > 0x7FFFFFFF || Hq > 0xFFFF || B > 0xFFFF)
-    return fail("sage_attn_fwd: invalid argument: shape too large");
+    return fail("%s: invalid argument: shape too large", who);
   if (blkk != 64 && blkk != 128 && blkk != 256)
-    return fail("sage_attn_fwd: invalid argument: blkk=%d (64, 128 or 256)", blkk);
+    return fail("%s: invalid argument: blkk=%d (64, 128 or 256)", who, blkk);
   if (q_sub < 32 || q_sub % 32 != 0 || blkq % q_sub != 0)
-    return fail("sage_attn_fwd: invalid argument: q_sub=%d blkq=%d (q_sub: a multiple of 32 dividing blkq)", q_sub,
-                blkq);
-  if (!q8 || !q_scale || !k8 || !k_scale || !v || !o || !q8_strides || !k8_strides || !o_strides)
-    return fail("sage_attn_fwd: invalid argument: null pointer");
+    return fail("%s: invalid argument: q_sub=%d blkq=%d (q_sub: a multiple of 32 dividing blkq)", who, q_sub, blkq);
+  if (!k_scale || !k8 || !v || !o || !q_strides || !k8_strides || !o_strides)
+    return fail("%s: invalid argument: null pointer", who);
   if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16 && pv_mode != SAGE_PV_FP8)
-    return fail("sage_attn_fwd: invalid argument: pv_mode %d", pv_mode);
-  if (!is_float_code(o_dtype)) return fail("sage_attn_fwd: invalid argument: o_dtype %d", o_dtype);
+    return fail("%s: invalid argument: pv_mode %d", who, pv_mode);
+  if (!is_float_code(o_dtype)) return fail("%s: invalid argument: o_dtype %d", who, o_dtype);
   if (v_dtype != SAGE_DTYPE_VTILES)
-    return fail("sage_attn_fwd: invalid argument: v_dtype %d (V must be in the tile layout of sage_vtiles)",
-                v_dtype);
-  if (pv_mode == SAGE_PV_FP8 && !v_scale)
-    return fail("sage_attn_fwd: invalid argument: FP8 P.V needs v_scale");
+    return fail("%s: invalid argument: v_dtype %d (V must be in the tile layout of sage_vtiles)", who, v_dtype);
+  if (pv_mode == SAGE_PV_FP8 && !v_scale) return fail("%s: invalid argument: FP8 P.V needs v_scale", who);
   const int oes = o_dtype == SAGE_DTYPE_F32 ? 4 : 2;
-  const bool rows32 = Nq * q8_strides[2] + D < 0x7FFFFFFF && Nkv * k8_strides[2] + D < 0x7FFFFFFF &&
+  const bool rows32 = (Nq * q_strides[2] + D) * q_es < 0x7FFFFFFF && Nkv * k8_strides[2] + D < 0x7FFFFFFF &&
                       Nq * o_strides[2] + D < 0x7FFFFFFF;
-  if (!rows32) return fail("sage_attn_fwd: invalid argument: a head's rows must span < 2^31 elements");
-  if (!strides_ok(q8_strides, 1) || !strides_ok(k8_strides, 1) || !strides_ok(o_strides, oes))
-    return fail("sage_attn_fwd: invalid argument: strides must keep 16-byte aligned rows");
-  if (((uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)v | (uintptr_t)o) % 16 != 0)
-    return fail("sage_attn_fwd: invalid argument: base pointers must be 16-byte aligned");
-
-  AttnArgs a{};
-  a.q8 = q8;
-  a.q_scale = q_scale;
+  if (!rows32) return fail("%s: invalid argument: a head's rows must span < 2^31 elements", who);
+  if (!strides_ok(q_strides, q_es) || !strides_ok(k8_strides, 1) || !strides_ok(o_strides, oes))
+    return fail("%s: invalid argument: strides must keep 16-byte aligned rows", who);
+  if (((uintptr_t)k8 | (uintptr_t)v | (uintptr_t)o) % 16 != 0)
+    return fail("%s: invalid argument: base pointers must be 16-byte aligned", who);
   a.k8 = k8;
   a.k_scale = k_scale;
   a.v = v;
   a.v_scale = v_scale;
   a.o = o;
   for (int i = 0; i < 2; ++i) {
-    a.sq[i] = q8_strides[i];
+    a.sq[i] = q_strides[i];
     a.sk[i] = k8_strides[i];
     a.so[i] = o_strides[i];
   }
-  a.sqn = (int)q8_strides[2];
+  a.sqn = (int)q_strides[2];
   a.skn = (int)k8_strides[2];
   a.son = (int)o_strides[2];
   a.B = (int)B;
@@ -667,12 +741,67 @@ extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const 
   a.blkk_shift = blkk == 64 ? 0 : (blkk == 128 ? 1 : 2);
   a.nqs = (int)(((Nq + blkq - 1) / blkq) * (blkq / q_sub));
   a.nks = (int)((Nkv + blkk - 1) / blkk);
+  return 0;
+}
+
+}  // namespace sage
+
+using namespace sage;
+
+extern "C" int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_scale,
+                             const int8_t* k8, const int64_t* k8_strides, const float* k_scale,
+                             const void* v, int v_dtype, const int64_t* v_strides, const float* v_scale,
+                             void* o, int o_dtype, const int64_t* o_strides, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq,
+                             int blkk, int q_sub, int pv_mode, void* stream) {
+  (void)v_strides;
+  const char* who = "sage_attn_fwd";
+  if (!q8 || !q_scale || !q8_strides) return fail("%s: invalid argument: null pointer", who);
+  AttnArgs a{};
+  if (int rc = attn_setup(a, who, q8_strides, 1, k8, k8_strides, k_scale, v, v_dtype, v_scale, o, o_dtype,
+                          o_strides, B, Hq, Hkv, Nq, Nkv, D, causal, blkq, blkk, q_sub, pv_mode))
+    return rc;
+  if ((uintptr_t)q8 % 16 != 0) return fail("%s: invalid argument: base pointers must be 16-byte aligned", who);
+  a.q8 = q8;
+  a.q_scale = q_scale;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int d = (int)D;
   switch (o_dtype) {
     case SAGE_DTYPE_F32: return launch_pv<float>(a, d, pv_mode, st);
     case SAGE_DTYPE_F16: return launch_pv<_Float16>(a, d, pv_mode, st);
     default: return launch_pv<__bf16>(a, d, pv_mode, st);
+  }
+}
+
+extern "C" int sage_attn_fwd_q(const void* q, const int64_t* q_strides, int q_dtype, float q_mul, int8_t* q8_out,
+                               float* q_scale_out, const int8_t* k8, const int64_t* k8_strides,
+                               const float* k_scale, const void* v, int v_dtype, const int64_t* v_strides,
+                               const float* v_scale, void* o, const int64_t* o_strides, int64_t B, int64_t Hq,
+                               int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, int causal, int blkq, int blkk,
+                               int q_sub, int pv_mode, void* stream) {
+  (void)v_strides;
+  const char* who = "sage_attn_fwd_q";
+  if (!q || !q_strides) return fail("%s: invalid argument: null pointer", who);
+  if (!is_float_code(q_dtype)) return fail("%s: invalid argument: q_dtype %d", who, q_dtype);
+  if (blkq != 128) return fail("%s: invalid argument: blkq=%d (128: the rows of 4 waves)", who, blkq);
+  if (!(q_mul > 0.0f) || q_mul == INFINITY) return fail("%s: invalid argument: q_mul %g", who, q_mul);
+  const int qes = q_dtype == SAGE_DTYPE_F32 ? 4 : 2;
+  AttnArgs a{};
+  if (int rc = attn_setup(a, who, q_strides, qes, k8, k8_strides, k_scale, v, v_dtype, v_scale, o, q_dtype,
+                          o_strides, B, Hq, Hkv, Nq, Nkv, D, causal, blkq, blkk, q_sub, pv_mode))
+    return rc;
+  if (((uintptr_t)q | (uintptr_t)q8_out) % 16 != 0)
+    return fail("%s: invalid argument: base pointers must be 16-byte aligned", who);
+  a.q8 = q;
+  a.q_mul = q_mul;
+  a.q8_out = q8_out;
+  a.qs_out = q_scale_out;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int d = (int)D;
+  switch (q_dtype) {
+    case SAGE_DTYPE_F32: return launch_pv_q<float>(a, d, pv_mode, st);
+    case SAGE_DTYPE_F16: return launch_pv_q<_Float16>(a, d, pv_mode, st);
+    default: return launch_pv_q<__bf16>(a, d, pv_mode, st);
   }
 }
 

@@ -50,20 +50,6 @@ struct PrepassArgs {
   int64_t n_kblk_b, n_qblk_b;          // role counts of launch B (K blocks first)
 };
 
-// ---------------------------------------------------------------------------
-// max of a non-negative value over the wave: DPP steps inside each 16-lane row
-// (quad xor 1, quad xor 2, half-row mirror, row mirror), then the four row
-// results via readlane.  Result is wave-uniform.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
-  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-  return max(max(r0, r1), max(r2, r3));
-}
 
 // ---------------------------------------------------------------------------
 // One quantization block: rows [0, rows_valid) of blk rows x D, scale per
@@ -450,14 +436,16 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
     return fail("sage_prepass: invalid argument: v_mode %d", v_mode);
   const bool vfp8 = v_mode != SAGE_V_NONE;  // V statistics and v_scale
   const bool vrows = v_mode == SAGE_V_FP8;  // row-major codes as well
-  if (!q || !k || !q8 || !k8 || !q_scale || !k_scale || !q_strides || !k_strides || !q8_strides ||
+  // q, q8 and q_scale all NULL: K (and V) only -- Q is quantized by sage_attn_fwd_q
+  const bool do_q = q || q8 || q_scale;
+  if ((do_q && (!q || !q8 || !q_scale || !q_strides || !q8_strides)) || !k || !k8 || !k_scale || !k_strides ||
       !k8_strides)
     return fail("sage_prepass: invalid argument: null pointer");
   if (smooth_k && !km) return fail("sage_prepass: invalid argument: km is null with smooth_k");
   if (vfp8 && (!v || !v_scale || !v_strides || (vrows && (!v8 || !v8_strides))))
     return fail("sage_prepass: invalid argument: null V pointer with v_mode %d", v_mode);
   const int es = in_dtype == SAGE_DTYPE_F32 ? 4 : 2;
-  if (!strides_ok(q_strides, es) || !strides_ok(k_strides, es) || !strides_ok(q8_strides, 1) ||
+  if ((do_q && (!strides_ok(q_strides, es) || !strides_ok(q8_strides, 1))) || !strides_ok(k_strides, es) ||
       !strides_ok(k8_strides, 1) || (vfp8 && !strides_ok(v_strides, es)) || (vrows && !strides_ok(v8_strides, 1)))
     return fail("sage_prepass: invalid argument: strides must keep 16-byte aligned rows");
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)(vfp8 ? v : nullptr) |
@@ -477,9 +465,9 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   a.Nq = Nq;
   a.Nkv = Nkv;
   for (int i = 0; i < 3; ++i) {
-    a.sq[i] = q_strides[i];
+    a.sq[i] = do_q ? q_strides[i] : 0;
     a.sk[i] = k_strides[i];
-    a.sq8[i] = q8_strides[i];
+    a.sq8[i] = do_q ? q8_strides[i] : 0;
     a.sk8[i] = k8_strides[i];
     a.sv[i] = vfp8 ? v_strides[i] : 0;
     a.sv8[i] = vrows ? v8_strides[i] : 0;
@@ -511,10 +499,10 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   // while it is likely still in the Infinity Cache) and Q.  Without
   // statistics everything runs in launch A.
   a.n_stat = need_b ? a.nch * Hkv * B : 0;
-  a.n_qblk_a = need_b ? 0 : a.nqb * Hq * B;
+  a.n_qblk_a = need_b || !do_q ? 0 : a.nqb * Hq * B;
   a.n_kblk_a = need_b ? 0 : a.nkb * Hkv * B;
   a.n_kblk_b = need_b ? a.nkb * Hkv * B : 0;
-  a.n_qblk_b = need_b ? a.nqb * Hq * B : 0;
+  a.n_qblk_b = need_b && do_q ? a.nqb * Hq * B : 0;
   if (a.n_stat + a.n_qblk_a + a.n_kblk_a > 0x7FFFFFFF || a.n_kblk_b + a.n_qblk_b > 0x7FFFFFFF)
     return fail("sage_prepass: invalid argument: grid too large");
 

@@ -26,7 +26,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
 
@@ -81,6 +81,11 @@ def _load():
     lib.sage_attn_fwd.restype = i32
     lib.sage_attn_fwd.argtypes = [
         vp, p64, vp, vp, p64, vp, vp, i32, p64, vp, vp, i32, p64, i64, i64, i64, i64, i64, i64, i32,
+        i32, i32, i32, i32, vp,
+    ]
+    lib.sage_attn_fwd_q.restype = i32
+    lib.sage_attn_fwd_q.argtypes = [
+        vp, p64, i32, f32, vp, vp, vp, p64, vp, vp, i32, p64, vp, vp, p64, i64, i64, i64, i64, i64, i64, i32,
         i32, i32, i32, i32, vp,
     ]
     lib.sage_flash_fwd.restype = i32
@@ -177,13 +182,14 @@ def vtiles(v, pv_dtype="fp16", v_scale=None, *, tensor_layout="HND"):
 
 
 def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smooth_k=True,
-            v_fp8=False, pv_dtype=None, tensor_layout="HND"):
+            v_fp8=False, pv_dtype=None, quant_q=True, tensor_layout="HND"):
     """Run the HIP pre-pass; returns a dict of device tensors.
 
     q8/k8 (int8, same layout as q/k), q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)],
     k_scale [B,Hkv,ceil(Nkv/blkk)], km [B,Hkv,D] (smooth_k), v8 (row-major e4m3
     codes as uint8) + v_scale [B,Hkv,D] (v_fp8), and with ``pv_dtype`` the V
-    tiles ``vt`` that :func:`attention` reads (v_scale too for "fp8").
+    tiles ``vt`` that :func:`attention` reads (v_scale too for "fp8").  With
+    ``quant_q=False`` Q is left to :func:`attention_q` (no q8 / q_scale).
     """
     lib = _load()
     B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v if v is not None else k, tensor_layout)
@@ -195,10 +201,10 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         sm_scale = D ** -0.5
     q_mul = float(np.float32(sm_scale * LOG2E_REF))
     dev = q.device
-    q8 = _empty_like_layout(q, torch.int8)
+    q8 = _empty_like_layout(q, torch.int8) if quant_q else None
     k8 = _empty_like_layout(k, torch.int8)
     nqs = -(-Nq // blkq) * (blkq // q_sub)
-    q_scale = torch.empty((B, Hq, nqs), dtype=torch.float32, device=dev)
+    q_scale = torch.empty((B, Hq, nqs), dtype=torch.float32, device=dev) if quant_q else None
     k_scale = torch.empty((B, Hkv, -(-Nkv // blkk)), dtype=torch.float32, device=dev)
     km = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev) if smooth_k else None
     v8 = v_scale = None
@@ -210,16 +216,20 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     uses_v = v_mode != V_NONE
     rc = lib.sage_prepass(
-        _ptr(q), _ptr(k), _ptr(v) if uses_v else None, _TORCH_CODES[q.dtype], B, Hq, Hkv, Nq, Nkv, D,
-        _strides(q, tensor_layout), _strides(k, tensor_layout),
+        _ptr(q) if quant_q else None, _ptr(k), _ptr(v) if uses_v else None, _TORCH_CODES[q.dtype], B, Hq, Hkv,
+        Nq, Nkv, D, _strides(q, tensor_layout) if quant_q else None, _strides(k, tensor_layout),
         _strides(v, tensor_layout) if uses_v else None,
         q_mul, blkq, blkk, q_sub, int(smooth_k), v_mode,
-        _ptr(q8), _strides(q8, tensor_layout), _ptr(q_scale), _ptr(k8), _strides(k8, tensor_layout),
+        _ptr(q8), _strides(q8, tensor_layout) if quant_q else None, _ptr(q_scale), _ptr(k8),
+        _strides(k8, tensor_layout),
         _ptr(k_scale), _ptr(km), _ptr(v8), _strides(v8, tensor_layout) if v_fp8 else None, _ptr(v_scale),
         _ptr(ws), ctypes.c_size_t(ws_bytes), _stream(dev),
     )
     _check(rc, "sage_prepass")
-    out = {"q8": q8, "q_scale": q_scale, "k8": k8, "k_scale": k_scale, "workspace": ws}
+    out = {"k8": k8, "k_scale": k_scale, "workspace": ws}
+    if quant_q:
+        out["q8"] = q8
+        out["q_scale"] = q_scale
     if smooth_k:
         out["km"] = km
     if v_fp8:
@@ -232,11 +242,11 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
 
 
 def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
-                  tensor_layout="HND", **kw):
+                  fuse_q=False, tensor_layout="HND", **kw):
     """The pre-pass of :func:`run` alone, with run's arguments (the harness
     times it as the ``prepass`` stage to report its HBM rate)."""
     q_sub = WAVE_ROWS if q_gran == "wave" else 128
-    return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, pv_dtype=pv_dtype,
+    return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, pv_dtype=pv_dtype, quant_q=not fuse_q,
                    tensor_layout=tensor_layout)
 
 
@@ -281,8 +291,40 @@ def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=12
     return o
 
 
+def attention_q(q, k, v, pre, causal=False, sm_scale=None, *, pv_dtype="fp16", q_sub=128, blkk=64,
+                tensor_layout="HND", out=None, q8_out=None, q_scale_out=None):
+    """The fused attention with the Q quantization of the pre-pass done in its
+    prologue (C-ABI sage_attn_fwd_q; BLKQ 128): ``pre`` from
+    :func:`prepass` with ``quant_q=False``.  ``q8_out`` / ``q_scale_out``
+    (optional) receive Q8 and q_scale.  Returns o with q's shape and dtype.
+    """
+    lib = _load()
+    if pv_dtype not in PV_MODES:
+        raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
+    B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
+    if sm_scale is None:
+        sm_scale = D ** -0.5
+    q_mul = float(np.float32(sm_scale * LOG2E_REF))
+    o = _empty_like_layout(q, q.dtype) if out is None else out
+    vt = pre.get("vt")
+    if vt is None:
+        vt = vtiles(v, pv_dtype, pre.get("v_scale"), tensor_layout=tensor_layout)
+    elif vt.numel() < lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype]):
+        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] is not a {pv_dtype} tile buffer")
+    if q8_out is not None and (q8_out.dtype != torch.int8 or q8_out.stride() != q.stride()):
+        raise ValueError("sage_attn hip: invalid argument: q8_out must be int8 with q's strides")
+    rc = lib.sage_attn_fwd_q(
+        _ptr(q), _strides(q, tensor_layout), _TORCH_CODES[q.dtype], ctypes.c_float(q_mul), _ptr(q8_out),
+        _ptr(q_scale_out), _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
+        _ptr(vt), DTYPE_VTILES, None, _ptr(pre.get("v_scale")), _ptr(o), _strides(o, tensor_layout),
+        B, Hq, Hkv, Nq, Nkv, D, int(bool(causal)), 128, blkk, q_sub, PV_MODES[pv_dtype], _stream(q.device),
+    )
+    _check(rc, "sage_attn_fwd_q")
+    return o
+
+
 def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
-        tensor_layout="HND", return_intermediates=False, **kw):
+        fuse_q=False, tensor_layout="HND", return_intermediates=False, **kw):
     """SageAttention forward on MI355X: INT8 QK^T, online softmax, P.V.
 
     Same call as run_sage_attn(q, k, v, causal=False, sm_scale=None)
@@ -295,6 +337,9 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
     q_gran     "block": one Q scale per 128 rows (reference); "wave": one per
                32 rows (the attention kernel's per-wavefront tile)
     smooth_k   subtract the per-channel K mean before quantizing (default on)
+    fuse_q     quantize Q in the attention kernel's prologue instead of the
+               pre-pass (the same Q8 and scales; off by default: on MI355X the
+               prologue work costs about what the pre-pass saves)
     """
     if pv_dtype not in PV_MODES:
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
@@ -304,9 +349,19 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
     blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
     q_sub = WAVE_ROWS if q_gran == "wave" else blkq
     pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k,
-                  pv_dtype=pv_dtype, tensor_layout=tensor_layout)
-    o = attention(q, k, v, pre, causal, pv_dtype=pv_dtype, q_sub=q_sub, blkq=blkq, blkk=blkk,
-                  tensor_layout=tensor_layout)
+                  pv_dtype=pv_dtype, quant_q=not fuse_q, tensor_layout=tensor_layout)
+    if fuse_q:
+        q8 = qs = None
+        if return_intermediates:
+            B, Hq, Nq, _ = _dims(q, tensor_layout)
+            q8 = _empty_like_layout(q, torch.int8)
+            qs = torch.empty((B, Hq, -(-Nq // blkq) * (blkq // q_sub)), dtype=torch.float32, device=q.device)
+            pre["q8"], pre["q_scale"] = q8, qs
+        o = attention_q(q, k, v, pre, causal, sm_scale, pv_dtype=pv_dtype, q_sub=q_sub, blkk=blkk,
+                        tensor_layout=tensor_layout, q8_out=q8, q_scale_out=qs)
+    else:
+        o = attention(q, k, v, pre, causal, pv_dtype=pv_dtype, q_sub=q_sub, blkq=blkq, blkk=blkk,
+                      tensor_layout=tensor_layout)
     if return_intermediates:
         pre.pop("workspace", None)
         pre.pop("vt", None)

@@ -103,9 +103,11 @@ def estimate(case: dict):
     ``flops`` is the reference's 4*B*H*N^2*D (the headline metric counts this
     even for causal cases); ``bytes`` is the reference's q, k, v, o at 2 bytes.
     Added: ``algo_flops`` (4*B*Hq*D*unmasked pairs), ``prepass_bytes`` (the
-    HBM floor of the quantization pre-pass) and ``vtile_bytes`` (the HBM floor
-    of converting V to the 16-bit P.V type, the reference's v.to(float16) of
-    triton_impl.py:189; 0 for FP8 P.V, whose V codes are in prepass_bytes).
+    HBM floor of the quantization pre-pass), ``prepass_bytes_k`` (the same
+    without Q, when the attention kernel quantizes Q itself) and
+    ``vtile_bytes`` (the HBM floor of converting V to the 16-bit P.V type,
+    the reference's v.to(float16) of triton_impl.py:189; 0 for FP8 P.V, whose
+    V codes are in prepass_bytes).
     """
     B = case.get("batch_size", 8)
     H = case.get("num_heads", 16)
@@ -118,17 +120,19 @@ def estimate(case: dict):
     in_bytes = 2
     eq, ek = B * H * N * D, B * Hkv * N * D
     q_sub = 32 if case.get("q_gran") == "wave" else 128
-    pre = in_bytes * (eq + ek) + (eq + ek)
-    pre += 4 * (B * H * math.ceil(N / 128) * (128 // q_sub) + B * Hkv * math.ceil(N / 64))
+    q_part = in_bytes * eq + eq + 4 * B * H * math.ceil(N / 128) * (128 // q_sub)
+    pre_k = in_bytes * ek + ek + 4 * B * Hkv * math.ceil(N / 64)
     if case.get("smooth_k", True):
-        pre += 4 * B * Hkv * D
+        pre_k += 4 * B * Hkv * D
     fp8 = case.get("pv_dtype") == "fp8"
     if fp8:
-        pre += in_bytes * ek + ek + 4 * B * Hkv * D
+        pre_k += in_bytes * ek + ek + 4 * B * Hkv * D
+    pre = q_part + pre_k
     return {
         "flops": flops,
         "bytes": 4 * B * H * N * D * 2,
         "algo_flops": 4 * B * H * D * pairs,
         "prepass_bytes": pre,
+        "prepass_bytes_k": pre_k,
         "vtile_bytes": 0 if fp8 else (in_bytes + 2) * ek,
     }
