@@ -468,7 +468,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
     // INT8: S reads as the float 2^23 + 2^22 + S, so S*c - m = that*c - bias
     const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
-    float ls[2];
+    // fp16 P: the row sum adds the fp16 values the P.V MFMAs consume, in a
+    // packed fp16 tree (15 v_pk_add_f16 instead of 32 fp32 adds; P <= 2^kTau,
+    // so the block's 32-term sum stays below 2^13 and its relative error below
+    // 5 * 2^-11), then one dot2 adds it into the fp32 lsum
+    constexpr bool kSumF16 = PVM == SAGE_PV_F16;
+    float ls[2] = {0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       float p[16];
@@ -486,13 +491,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int w = 0; w < 8; ++w) P[8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
       }
+      if constexpr (!kSumF16) {
 #pragma unroll
-      for (int w = 8; w >= 1; w >>= 1)
+        for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
-        for (int i = 0; i < w; ++i) p[i] += p[i + w];
-      ls[t] = p[0];
+          for (int i = 0; i < w; ++i) p[i] += p[i + w];
+        ls[t] = p[0];
+      }
     }
-    lsum += ls[0] + ls[1];
+    if constexpr (kSumF16) {
+      h2 hs[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) hs[w] = __builtin_bit_cast(h2, P[w]) + __builtin_bit_cast(h2, P[8 + w]);
+#pragma unroll
+      for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) hs[i] = hs[i] + hs[i + w];
+      lsum = __builtin_amdgcn_fdot2(hs[0], (h2){(_Float16)1.0f, (_Float16)1.0f}, lsum, false);
+    } else {
+      lsum += ls[0] + ls[1];
+    }
   };
   auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
