@@ -306,8 +306,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // chunk (physical chunk ^ swizzle of its row).  K8 rows past Nkv read the
   // last row (their P is 0); V^T tiles are zero past Nkv.  Loads past the
   // tile go to the sink, so every wave issues LPW loads per tile.
-  auto load_tile = [&](int j) __attribute__((always_inline)) {
-    char* slot = smem + (j % NBUF) * SLOT;
+  auto load_tile = [&](int j, int sl) __attribute__((always_inline)) {  // sl = j % NBUF
+    char* slot = smem + sl * SLOT;
     const int k0 = j * kBN;
     const uint8_t* vt = vtbase + (int64_t)j * VTB;
 #pragma unroll
@@ -353,8 +353,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   SAcc S[2];             // S^T of key tiles 0 and 1 of the block in flight
   float ksc_cur = 0.0f;  // k scale of the block held in S (INT8)
   uint32_t Pprev[PW], Pcur[PW];  // P of blocks j-1 and j
-  const v16i magic = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
-                      kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
+  v16i magic = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
+                kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
+  // held in VGPRs for the whole kernel, so that the first MFMA of each S tile
+  // reads it as srcC (the compiler would rebuild it from SGPRs every block);
+  // measured faster with FP8 P and at D = 64, slower at D = 128 with fp16 P
+  if constexpr (kI8 && (PVM == SAGE_PV_FP8 || D == 64)) asm volatile("" : "+v"(magic));
 
   // per-lane byte offsets of the swizzled operand chunks
   int koff[KC];  // K row 32t + n (swizzle independent of t), logical chunk 2c + hh
@@ -367,8 +371,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // ---- building blocks
   // S^T of block j (its K tile in slot j % NBUF): K row 32t + n, bytes 32c + 16hh
-  auto qk = [&](int j) __attribute__((always_inline)) {
-    const char* ks = smem + (j % NBUF) * SLOT;
+  auto qk = [&](int j, int sl) __attribute__((always_inline)) {  // sl = j % NBUF
+    const char* ks = smem + sl * SLOT;
     if constexpr (kI8) ksc_cur = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -391,8 +395,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
   };
   // O^T += V^T P^T of block j (its V^T tile in slot j % NBUF)
-  auto pv = [&](int j, const uint32_t (&P)[PW]) __attribute__((always_inline)) {
-    const char* vs = smem + (j % NBUF) * SLOT;
+  auto pv = [&](int sl, const uint32_t (&P)[PW]) __attribute__((always_inline)) {  // sl = j % NBUF
+    const char* vs = smem + sl * SLOT;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
       const char* vr = vs + 32 * dt * VRB;
@@ -528,34 +532,36 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // iterations.  The mask-free steady state has a loop of its own so that the
   // O accumulators are updated from one place in each loop.
   auto generic_iter = [&](int j) __attribute__((always_inline)) {
-    if (j + 3 < nkb) load_tile(j + 3);
+    if (j + 3 < nkb) load_tile(j + 3, (j + 3) % NBUF);
     if (pend) {
       rescale_o();
       pend = false;
     }
-    if (j >= 1 && j - 1 <= jmax) pv(j - 1, Pprev);
+    if (j >= 1 && j - 1 <= jmax) pv((j - 1) % NBUF, Pprev);
     __builtin_amdgcn_sched_barrier(0);
     if (j <= jmax) {
       if (j < nfull) softmax(j, Pcur, false);
       else softmax(j, Pcur, true);
       keep_p();
     }
-    if (j + 1 <= jmax) qk(j + 1);
+    if (j + 1 <= jmax) qk(j + 1, (j + 1) % NBUF);
     sync_tiles(j + 3 < nkb);
   };
   // blocks 1 <= j < j_fast: every stage exists and no mask is needed; the P.V
   // MFMAs of block j-1 and the softmax VALU work of block j share one basic
   // block for the scheduler to interleave
-  auto fast_iter = [&](int j) __attribute__((always_inline)) {
-    load_tile(j + 3);
+  // sl: j % NBUF as a constant (the unrolled loop: operand offsets fold into
+  // the LDS instructions), or -1 to compute the slots from j
+  auto fast_iter = [&](int j, int sl) __attribute__((always_inline)) {
+    load_tile(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
     if (pend) {
       rescale_o();
       pend = false;
     }
-    pv(j - 1, Pprev);
+    pv(sl < 0 ? (j - 1) % NBUF : (sl + NBUF - 1) % NBUF, Pprev);
     softmax(j, Pcur, false);
     keep_p();
-    qk(j + 1);
+    qk(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF);
     sync_tiles(true);
   };
 
@@ -611,17 +617,28 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // With fewer than 3 tiles the last one is requested again (same data into
   // its own slot), so the number of loads issued after Q's is fixed and Q can
   // be waited for without draining the tile loads.
-  load_tile(0);
-  load_tile(min(1, nkb - 1));
-  load_tile(min(2, nkb - 1));
+  load_tile(0, 0);
+  load_tile(min(1, nkb - 1), min(1, nkb - 1));
+  load_tile(min(2, nkb - 1), min(2, nkb - 1));
   quantize_q();
   sync_tiles(nkb > 2);
-  if (jmax >= 0) qk(0);
+  if (jmax >= 0) qk(0, 0);
 
   const int j_fast = min(min(nfull, jmax), nkb - 3);
   generic_iter(0);
   int j = 1;
-  for (; j < j_fast; ++j) fast_iter(j);
+  // INT8 at D = 64 with fp16 P: five iterations per trip with constant ring
+  // slots (elsewhere the copies run out of registers); j % NBUF == 1 at every
+  // trip
+  if constexpr (kI8 && D == 64 && PVM == SAGE_PV_F16)
+    for (; j + NBUF <= j_fast; j += NBUF) {
+      fast_iter(j, 1);
+      fast_iter(j + 1, 2);
+      fast_iter(j + 2, 3);
+      fast_iter(j + 3, 4);
+      fast_iter(j + 4, 0);
+    }
+  for (; j < j_fast; ++j) fast_iter(j, -1);
   for (; j <= nkb; ++j) generic_iter(j);
 
   // ---- epilogue: O / l, store row q = qa + n, d = 32dt + 8i + 4hh .. +4
