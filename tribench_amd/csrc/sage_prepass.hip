@@ -59,7 +59,7 @@ struct PrepassArgs {
 // (blk * D / 4096, at least 1; with fewer items than threads whole waves idle).
 // ---------------------------------------------------------------------------
 template <typename T, int D, int NI>
-__device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
+__device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
                             int q_sub, bool use_mul, float mul, const float* km_s,
                             int8_t* __restrict__ dst, int64_t dn, float* __restrict__ scale_dst,
                             uint32_t* amax_s, float* scl_s, float* rcp_s) {
@@ -161,7 +161,7 @@ __device__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_vali
 // sage_quant_math.h, and (if vsrc) channel max|v|.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__device__ void kstats_chunk(const T* __restrict__ ksrc, int64_t ksn, const T* __restrict__ vsrc,
+__device__ __forceinline__ void kstats_chunk(const T* __restrict__ ksrc, int64_t ksn, const T* __restrict__ vsrc,
                              int64_t vsn, int64_t n0, int64_t n1, float* __restrict__ psum,
                              float* __restrict__ pamax, float* red_s) {
   constexpr int CG = D / 8;
@@ -243,7 +243,7 @@ __device__ void kstats_chunk(const T* __restrict__ ksrc, int64_t ksn, const T* _
 // FP8 e4m3 V block: v8 = RNE_sat(v / v_scale[c]) (v_scale[c] == 0 -> 0)
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__device__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
+__device__ __forceinline__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
                              const float* vs_s, uint8_t* __restrict__ dst, int64_t dn) {
   constexpr int CPR = D / 16;
   const int nit = blk * CPR;
@@ -265,7 +265,7 @@ __device__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_val
 }
 
 template <typename T, int D, int NI>
-__device__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, float* scl_s,
+__device__ __forceinline__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, float* scl_s,
                              float* rcp_s) {
   const int64_t qb = r % a.nqb, h = (r / a.nqb) % a.Hq, b = r / (a.nqb * a.Hq);
   const int64_t row0 = qb * a.blkq;
@@ -279,7 +279,7 @@ __device__ void quant_q_role(const PrepassArgs& a, int64_t r, uint32_t* amax_s, 
 }
 
 template <typename T, int D, int NI>
-__device__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s, uint32_t* amax_s,
+__device__ __forceinline__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s, uint32_t* amax_s,
                              float* scl_s, float* rcp_s) {
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
   const int64_t row0 = kb * a.blkk;
