@@ -142,7 +142,7 @@ def main(argv=None) -> int:
     q, k, v = (inp[x].to(dev) for x in ("q", "k", "v"))
     causal = bool(inp["causal"])
     pv = case.get("pv_dtype", "fp16")
-    q_sub = H.WAVE_ROWS if case.get("q_gran") == "wave" else 128
+    q_sub = H.q_sub_of(case.get("q_gran", "block"))
     B, Hq, N, D = q.shape
     est = R.estimate(case)
     metric_ops, algo_ops = float(est["flops"]), float(est["algo_flops"])

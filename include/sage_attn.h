@@ -90,8 +90,10 @@ size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t Nkv, int64_t
  *            reference passes fp32(sm_scale * 1.44269504) (triton_impl.py:69)
  *  blkq/blkk rows per scale block (reference: 128 / 64); 16 <= blk <= 256,
  *            multiples of 16
- *  q_sub     rows per Q scale: blkq (one scale per block, the reference) or a
- *            divisor of blkq that is a multiple of 16 (per-wave scales)
+ *  q_sub     rows per Q scale: blkq (one scale per block, the reference), a
+ *            divisor of blkq that is a multiple of 16 (per-wave scales), or 1
+ *            (one scale per row: the rows one lane of the attention kernel's
+ *            MFMA operand holds)
  *  smooth_k  1: km[c] = mean over tokens of k[..,c] (fp32, fixed reduction
  *            order), K is quantized as fp32(k) - km[c]
  *  outputs   q8 [B,Hq,Nq,D] int8 + q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)]
@@ -143,7 +145,7 @@ int sage_vtiles(const void* v, int in_dtype, int64_t B, int64_t Hkv, int64_t Nkv
  *  causal 1: key j is visible to query i iff j <= i (top-left aligned, the
  *         torch.tril mask of reference.py:19-22)
  *  GQA    query head h reads KV head h / (Hq/Hkv) (triton_impl.py:137,145,147)
- *  blkk must be 64, 128 or 256; q_sub a multiple of 32 that divides blkq.
+ *  blkk must be 64, 128 or 256; q_sub 1 or a multiple of 32 that divides blkq.
  */
 int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_scale,
                   const int8_t* k8, const int64_t* k8_strides, const float* k_scale,
@@ -160,7 +162,7 @@ int sage_attn_fwd(const int8_t* q8, const int64_t* q8_strides, const float* q_sc
  *
  *  q [B,Hq,Nq,D] in q_dtype (F32/F16/BF16); o has q's type, o_strides its own
  *  q_mul     fp32(sm_scale * 1.44269504), as for sage_prepass
- *  blkq      must be 128 (four 32-row waves); q_sub 32, 64 or 128
+ *  blkq      must be 128 (four 32-row waves); q_sub 1, 32, 64 or 128
  *  q8_out, q_scale_out  optional (NULL: not written): Q8 with q's element
  *            strides and q_scale [B,Hq,ceil(Nq/128)*(128/q_sub)]
  *  everything else as sage_attn_fwd.

@@ -63,6 +63,8 @@ def _prepass_args(**over):
     (dict(B=0), "empty shape"),
     (dict(blkq=100), "blkq"),
     (dict(q_sub=48), "q_sub"),
+    (dict(q_sub=2), "q_sub"),
+    (dict(q_sub=0), "q_sub"),
     (dict(in_dtype=7), "in_dtype"),
     (dict(smooth=1), "km is null"),
     (dict(q=None), "null pointer"),
@@ -140,6 +142,7 @@ def test_attn_fwd_q_rejects_bad_arguments(lib):
     for over, needle in [
         (dict(blkq=64, q_sub=64), "blkq"),
         (dict(q_sub=48), "q_sub"),
+        (dict(q_sub=2), "q_sub"),
         (dict(qdt=9), "q_dtype"),
         (dict(qmul=-1.0), "q_mul"),
         (dict(vdt=2), "v_dtype"),

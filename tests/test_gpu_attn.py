@@ -57,6 +57,9 @@ SMALL = [
     (1, 2, 2, 1000, 128, "fp16", True, "fp16", "wave", 2.0),
     (1, 1, 1, 1, 64, "bf16", False, "fp16", "block", 0.0),     # single token
     (1, 2, 1, 65, 128, "bf16", True, "fp16", "block", 2.0),    # one full + one tail key block
+    (2, 4, 2, 300, 128, "bf16", True, "fp16", "thread", 2.0),  # per-row Q scales
+    (1, 3, 3, 1000, 64, "fp16", False, "fp16", "thread", 4.0),
+    (1, 2, 2, 777, 128, "bf16", True, "fp16", "thread", 2.0),
 ]
 
 
@@ -77,7 +80,7 @@ def test_attn_small_vs_oracle(case, pack_ref, hip_impl, gpu_device):
     got = o.float().cpu().numpy()
     assert np.isfinite(got).all()
     want = O.sdpa(inp["q"].float().numpy(), inp["k"].float().numpy(), inp["v"].float().numpy(), causal=causal)
-    q_sub = hip_impl.WAVE_ROWS if q_gran == "wave" else 128
+    q_sub = hip_impl.q_sub_of(q_gran)
     emu = O.sage_emulate(pre["q8"].cpu().numpy(), pre["q_scale"].cpu().numpy(), pre["k8"].cpu().numpy(),
                          pre["k_scale"].cpu().numpy(), inp["v"].float().numpy(), causal=causal, q_sub=q_sub)
     max_abs_e, cos_e = _metrics(got, emu)
@@ -111,6 +114,8 @@ FUSED = [
     (1, 3, 3, 1000, 64, "fp16", False, "wave", "HND"),
     (1, 2, 2, 777, 128, "fp32", False, "block", "NHD"),
     (1, 6, 1, 129, 64, "bf16", True, "wave", "NHD"),
+    (2, 4, 2, 300, 128, "bf16", True, "thread", "HND"),
+    (1, 2, 2, 1000, 64, "fp16", False, "thread", "NHD"),
 ]
 
 
@@ -129,7 +134,7 @@ def test_fused_q_matches_prepass(case, pack_ref, hip_impl, gpu_device):
     torch.cuda.synchronize()
     assert torch.equal(pre1["q8"], pre2["q8"]) and torch.equal(pre1["q_scale"], pre2["q_scale"])
     assert torch.equal(o1, o2)
-    q_sub = hip_impl.WAVE_ROWS if q_gran == "wave" else 128
+    q_sub = hip_impl.q_sub_of(q_gran)
     wq8, wqs = O.quant_per_block_int8(inp["q"].float().numpy(), 128, mul=O.q_multiplier(D), q_sub=q_sub)
     got_q8 = pre1["q8"].transpose(1, 2) if layout == "NHD" else pre1["q8"]
     assert np.array_equal(got_q8.cpu().numpy(), wq8) and np.array_equal(pre1["q_scale"].cpu().numpy(), wqs)

@@ -25,6 +25,8 @@ CASES = [
     (2, 6, 1, 777, 128, "bf16", 32, True, True, 2.0, "student_t"),    # FP8 V, GQA 6:1
     (1, 4, 4, 4096, 128, "bf16", 128, True, False, 2.0, "normal"),    # 16 K-stat chunks
     (1, 2, 2, 17776, 64, "bf16", 128, True, True, 2.0, "normal"),     # config-4 length, 14 chunks
+    (2, 4, 2, 300, 128, "bf16", 1, True, False, 2.0, "normal"),       # per-row Q scales, ragged
+    (1, 3, 3, 1000, 64, "fp16", 1, True, False, 4.0, "student_t"),    # per-row Q scales, D=64
 ]
 
 

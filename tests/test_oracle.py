@@ -98,7 +98,7 @@ def test_quant_matches_scalar_restatement(seed):
 def test_quant_invariants_and_error_bound():
     rng = np.random.default_rng(7)
     x = (rng.standard_normal((2, 3, 300, 64)) * 3 + rng.standard_normal((2, 3, 1, 64))).astype(np.float32)
-    for blk, q_sub in ((128, 128), (128, 32), (64, 64)):
+    for blk, q_sub in ((128, 128), (128, 32), (64, 64), (128, 1)):
         q8, sc = O.quant_per_block_int8(x, blk, q_sub=q_sub)
         assert np.abs(q8.astype(np.int32)).max() <= 127
         nsub = sc.shape[-1]
@@ -109,6 +109,21 @@ def test_quant_invariants_and_error_bound():
         s_rows = np.repeat(sc, q_sub, axis=-1)[:, :, :300, None].astype(np.float64)
         err = np.abs(q8 * s_rows - x)
         assert np.all(err <= s_rows * 0.5 * (1 + 2.0 ** -20) + 1e-38)
+
+
+def test_quant_per_row_is_blocks_of_one_row():
+    """One scale per row (q_sub = 1) inside 128-row blocks is the same
+    quantization as blocks of a single row, and padded rows get scale 0."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((2, 3, 300, 64)) * 2 + rng.standard_normal((2, 3, 300, 1)) * 5).astype(np.float32)
+    mul = O.q_multiplier(64)
+    q8, sc = O.quant_per_block_int8(x, 128, mul=mul, q_sub=1)
+    q8r, scr = O.quant_per_block_int8(x, 1, mul=mul)
+    assert np.array_equal(q8, q8r)
+    assert sc.shape == (2, 3, 384) and np.array_equal(sc[:, :, :300], scr) and np.all(sc[:, :, 300:] == 0)
+    # a row's scale is its own max|x * mul| / 127, independent of the other rows
+    xm = (x.astype(np.float32) * mul).astype(np.float32)
+    assert np.array_equal(sc[:, :, :300], (np.abs(xm).max(-1) / np.float32(127)).astype(np.float32))
 
 
 def test_quant_exact_on_grid():
@@ -262,7 +277,7 @@ def test_emulation_is_base2_sdpa_of_dequantized_inputs():
     q = rng.standard_normal((B, Hq, N, D)).astype(np.float32)
     k = (rng.standard_normal((B, Hkv, N, D)) + 2).astype(np.float32)
     v = rng.standard_normal((B, Hkv, N, D))
-    for q_sub in (128, 32):
+    for q_sub in (128, 32, 1):
         q8, qs = O.quant_per_block_int8(q, 128, mul=O.q_multiplier(D), q_sub=q_sub)
         k8, ks = O.quant_per_block_int8(k, 64)
         qd = q8 * np.repeat(qs, q_sub, axis=-1)[:, :, :N, None].astype(np.float64)

@@ -270,7 +270,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
     for (int c = 0; c < KC; ++c)
       qreg[c] = *reinterpret_cast<const v4i*>(qbase + (uint32_t)(row * a.sqn * QEB + 32 * c + 16 * hh));
-    if constexpr (kI8) qsc = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qa / a.q_sub, a.nqs - 1)];
+    if constexpr (kI8) {  // q_sub == 1: one scale per row, i.e. per lane column
+      const int qi = a.q_sub == 1 ? qa + n : qa / a.q_sub;
+      qsc = a.q_scale[((int64_t)b * a.Hq + h) * a.nqs + min(qi, a.nqs - 1)];
+    }
   }
   // Q quantized here (kFQ): its raw rows are requested now, the quantization
   // runs in the prologue once the first tiles are requested too, so the Q
@@ -585,7 +588,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           xq[c][e] = elem<TO>(qraw[c][e >> 3], e & 7) * a.q_mul;
           am = fmaxf(am, fabsf(xq[c][e]));
         }
-      am = __uint_as_float(wave_max_u32(__float_as_uint(valid ? am : 0.0f)));  // the wave's 32 rows
+      if (a.q_sub == 1) {  // one scale per row: its two lane halves
+        am = max_halves_f(valid ? am : 0.0f);
+      } else {
+        am = __uint_as_float(wave_max_u32(__float_as_uint(valid ? am : 0.0f)));  // the wave's 32 rows
+      }
       if (a.q_sub > 32) {  // a scale spans q_sub / 32 waves
         if (lane == 0) qamax_s[wave] = am;
         SAGE_WAIT_LGKM0();
@@ -607,9 +614,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
           *reinterpret_cast<v4i*>(a.q8_out + b * a.sq[0] + h * a.sq[1] + (int64_t)row * a.sqn + 32 * c + 16 * hh) =
               qreg[c];
       }
-      // every sub-block of the ceil(Nq/128) blocks, those with no rows too (scale 0)
-      if (a.qs_out && lane == 0 && qa < (a.Nq + 127) / 128 * 128 && qa % a.q_sub == 0)
-        a.qs_out[((int64_t)b * a.Hq + h) * a.nqs + qa / a.q_sub] = qsc;
+      // every sub-block (row) of the ceil(Nq/128) blocks, those with no rows too (scale 0)
+      if (a.qs_out && qa < (a.Nq + 127) / 128 * 128) {
+        float* qs = a.qs_out + ((int64_t)b * a.Hq + h) * a.nqs;
+        if (a.q_sub == 1) {
+          if (hh == 0) qs[row] = qsc;
+        } else if (lane == 0 && qa % a.q_sub == 0) {
+          qs[qa / a.q_sub] = qsc;
+        }
+      }
     }
   };
 
@@ -735,8 +748,9 @@ static int attn_setup(AttnArgs& a, const char* who, const int64_t* q_strides, in
     return fail("%s: invalid argument: shape too large", who);
   if (blkk != 64 && blkk != 128 && blkk != 256)
     return fail("%s: invalid argument: blkk=%d (64, 128 or 256)", who, blkk);
-  if (q_sub < 32 || q_sub % 32 != 0 || blkq % q_sub != 0)
-    return fail("%s: invalid argument: q_sub=%d blkq=%d (q_sub: a multiple of 32 dividing blkq)", who, q_sub, blkq);
+  if (q_sub != 1 && (q_sub < 32 || q_sub % 32 != 0 || blkq % q_sub != 0))
+    return fail("%s: invalid argument: q_sub=%d blkq=%d (q_sub: 1 or a multiple of 32 dividing blkq)", who, q_sub,
+                blkq);
   if (!k_scale || !k8 || !v || !o || !q_strides || !k8_strides || !o_strides)
     return fail("%s: invalid argument: null pointer", who);
   if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16 && pv_mode != SAGE_PV_FP8)

@@ -113,6 +113,18 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return max(max(r0, r1), max(r2, r3));
 }
 
+// max of a non-negative value over each group of W consecutive lanes (W = 4
+// or 8: quad xor 1, quad xor 2, then the half-row mirror for 8); every lane
+// of a group gets the group's max
+template <int W>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+  static_assert(W == 4 || W == 8, "group of 4 or 8 lanes");
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  if constexpr (W == 8) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  return v;
+}
+
 }  // namespace sage
 
 // ---------------------------------------------------------------------------

@@ -53,7 +53,8 @@ struct PrepassArgs {
 
 // ---------------------------------------------------------------------------
 // One quantization block: rows [0, rows_valid) of blk rows x D, scale per
-// q_sub rows (q_sub == blk: one scale per block, triton_impl.py:28,33).
+// q_sub rows (q_sub == blk: one scale per block, triton_impl.py:28,33;
+// q_sub == 1: one scale per row).
 // x = fp32(in) * mul (if use_mul) - km[c] (if km); tail rows are left out of
 // the block max and not stored.  NI = 16-element items per thread
 // (blk * D / 4096, at least 1; with fewer items than threads whole waves idle).
@@ -100,6 +101,42 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
       }
     }
     amx[j] = am;
+  }
+  if (q_sub == 1) {  // (block-uniform) a row's CPR items sit in consecutive lanes
+    float sc[NI], rc[NI];
+    bool ok = true;
+#pragma unroll
+    for (int j = 0; j < NI; ++j) {
+      const int it = tid + kPrepassThreads * j;
+      const int row = it / CPR;
+      sc[j] = block_scale(__uint_as_float(group_max_u32<CPR>(__float_as_uint(amx[j]))));
+      rc[j] = sc[j] > 0.0f ? 1.0f / sc[j] : 0.0f;
+      if (it < nit && it % CPR == 0) scale_dst[row] = sc[j];  // every row of the block (0 past the tail)
+      if (it < nit && row < rows_valid) ok = ok && fast_div_ok(sc[j]);
+    }
+    // one wave-uniform choice of the division, as below
+    auto quantize_rows = [&](auto fast_tag) __attribute__((always_inline)) {
+      constexpr bool kFast = decltype(fast_tag)::value;
+#pragma unroll
+      for (int j = 0; j < NI; ++j) {
+        const int it = tid + kPrepassThreads * j;
+        const int row = it / CPR, c = it % CPR;
+        if (it >= nit || row >= rows_valid) continue;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          float x = elem<T>(raw[j][e >> 3], e & 7);
+          if (use_mul) x = x * mul;
+          if (km_s) x = x - km_s[c * 16 + e];
+          const int8_t qv = quant_elem(x, sc[j], rc[j], kFast);
+          w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
+        }
+        *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      }
+    };
+    if (__builtin_amdgcn_ballot_w64(!ok) == 0) quantize_rows(std::true_type{});
+    else quantize_rows(std::false_type{});
+    return;
   }
   __syncthreads();  // amax_s cleared
   if (nsub == 1) {
@@ -430,7 +467,7 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   auto blk_ok = [](int b) { return b >= 16 && b <= 256 && b % 16 == 0; };
   if (!blk_ok(blkq) || !blk_ok(blkk))
     return fail("sage_prepass: invalid argument: blkq=%d blkk=%d (16..256, multiples of 16)", blkq, blkk);
-  if (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0 || blkq / q_sub > 16)
+  if (q_sub != 1 && (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0 || blkq / q_sub > 16))
     return fail("sage_prepass: invalid argument: q_sub=%d for blkq=%d", q_sub, blkq);
   if (v_mode != SAGE_V_NONE && v_mode != SAGE_V_FP8 && v_mode != SAGE_V_FP8_SCALE)
     return fail("sage_prepass: invalid argument: v_mode %d", v_mode);

@@ -29,6 +29,10 @@ import torch
 ABI_VERSION = 4
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
+# rows per Q scale for each q_gran: one block of 128 rows (the reference), one
+# wavefront's 32 rows, or one row (the rows one lane of the kernel's MFMA
+# operand holds, the counterpart of SageAttention's per-thread granularity)
+Q_GRAN_ROWS = {"block": 128, "wave": WAVE_ROWS, "thread": 1}
 
 DTYPE_F32, DTYPE_F16, DTYPE_BF16, DTYPE_FP8E4M3, DTYPE_VTILES = 0, 1, 2, 3, 4
 V_NONE, V_FP8, V_FP8_SCALE = 0, 1, 2
@@ -241,11 +245,18 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
     return out
 
 
+def q_sub_of(q_gran):
+    """Rows per Q scale for a q_gran option (raises on an unknown one)."""
+    if q_gran not in Q_GRAN_ROWS:
+        raise ValueError(f"sage_attn hip: invalid argument: q_gran {q_gran!r}")
+    return Q_GRAN_ROWS[q_gran]
+
+
 def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
                   fuse_q=False, tensor_layout="HND", **kw):
     """The pre-pass of :func:`run` alone, with run's arguments (the harness
     times it as the ``prepass`` stage to report its HBM rate)."""
-    q_sub = WAVE_ROWS if q_gran == "wave" else 128
+    q_sub = q_sub_of(q_gran)
     return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, pv_dtype=pv_dtype, quant_q=not fuse_q,
                    tensor_layout=tensor_layout)
 
@@ -335,7 +346,8 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
     pv_dtype   "fp16" (the reference's P.V type), "bf16", or "fp8" (FP8 e4m3 P
                and per-channel FP8 V)
     q_gran     "block": one Q scale per 128 rows (reference); "wave": one per
-               32 rows (the attention kernel's per-wavefront tile)
+               32 rows (the attention kernel's per-wavefront tile); "thread":
+               one per row (each lane of the kernel holds one query row)
     smooth_k   subtract the per-channel K mean before quantizing (default on)
     fuse_q     quantize Q in the attention kernel's prologue instead of the
                pre-pass (the same Q8 and scales; off by default: on MI355X the
@@ -343,11 +355,9 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
     """
     if pv_dtype not in PV_MODES:
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
-    if q_gran not in ("block", "wave"):
-        raise ValueError(f"sage_attn hip: invalid argument: q_gran {q_gran!r}")
+    q_sub = q_sub_of(q_gran)
     _check_inputs(q, k, v, tensor_layout)
     blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
-    q_sub = WAVE_ROWS if q_gran == "wave" else blkq
     pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k,
                   pv_dtype=pv_dtype, quant_q=not fuse_q, tensor_layout=tensor_layout)
     if fuse_q:

@@ -119,7 +119,7 @@ def estimate(case: dict):
     pairs = N * (N + 1) // 2 if causal else N * N
     in_bytes = 2
     eq, ek = B * H * N * D, B * Hkv * N * D
-    q_sub = 32 if case.get("q_gran") == "wave" else 128
+    q_sub = {"wave": 32, "thread": 1}.get(case.get("q_gran"), 128)  # rows per Q scale
     q_part = in_bytes * eq + eq + 4 * B * H * math.ceil(N / 128) * (128 // q_sub)
     pre_k = in_bytes * ek + ek + 4 * B * Hkv * math.ceil(N / 64)
     if case.get("smooth_k", True):
