@@ -660,21 +660,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const float* vsc = kF8 ? a.v_scale + ((int64_t)b * a.Hkv + hk) * D : nullptr;
   const float inv = 1.0f / sum_halves(lsum);
   const int row = qa + n;
-  if (row < a.Nq) {
+  auto out4 = [&](int dt, int i, TO* p) __attribute__((always_inline)) {
+    const int d0 = 32 * dt + 8 * i + 4 * hh;
+    float4 f = make_float4(inv, inv, inv, inv);
+    if constexpr (kF8) {
+      const float4 vs4 = *reinterpret_cast<const float4*>(vsc + d0);
+      f = make_float4(inv * vs4.x, inv * vs4.y, inv * vs4.z, inv * vs4.w);
+    }
+    const v16f& o = oacc[dt];
+    store4<TO>(p + d0, o[4 * i] * f.x, o[4 * i + 1] * f.y, o[4 * i + 2] * f.z, o[4 * i + 3] * f.w);
+  };
+  // The C layout gives each lane 8- or 16-byte pieces of 32 rows; written to
+  // HBM directly that is 32 partial lines per store.  Where the wave's 32 x D
+  // tile fits in its share of the (by now idle: the last iteration ended
+  // with LDS reads and tile loads drained and a barrier) tile ring, it goes
+  // through LDS and leaves as whole rows, 16 bytes per lane.
+  constexpr int ORP = D * (int)sizeof(TO) + 16;  // LDS row pitch: rows 4 banks apart
+  if constexpr (NW * 32 * ORP <= NBUF * SLOT) {
+    char* st = smem + wave * 32 * ORP;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int d0 = 32 * dt + 8 * i + 4 * hh;
-        float4 f = make_float4(inv, inv, inv, inv);
-        if constexpr (kF8) {
-          const float4 vs4 = *reinterpret_cast<const float4*>(vsc + d0);
-          f = make_float4(inv * vs4.x, inv * vs4.y, inv * vs4.z, inv * vs4.w);
-        }
-        const v16f& o = oacc[dt];
-        store4<TO>(obase + (uint32_t)(row * a.son + d0), o[4 * i] * f.x, o[4 * i + 1] * f.y, o[4 * i + 2] * f.z,
-                   o[4 * i + 3] * f.w);
-      }
+      for (int i = 0; i < 4; ++i) out4(dt, i, reinterpret_cast<TO*>(st + n * ORP));
+    constexpr int CPO = D * (int)sizeof(TO) / 16;  // 16-byte chunks per row
+    constexpr int RPI = 64 / CPO;                  // rows per instruction
+    const int rr = lane / CPO, cc = lane % CPO;
+#pragma unroll
+    for (int r0 = 0; r0 < 32; r0 += RPI) {
+      const v4i val = *reinterpret_cast<const v4i*>(st + (r0 + rr) * ORP + 16 * cc);
+      const int orow = qa + r0 + rr;
+      if (orow < a.Nq)
+        *reinterpret_cast<v4i*>(reinterpret_cast<char*>(obase + (uint32_t)(orow * a.son)) + 16 * cc) = val;
+    }
+  } else if (row < a.Nq) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) out4(dt, i, obase + (uint32_t)(row * a.son));
   }
 }
 
