@@ -10,6 +10,7 @@
  *                         + FP8 V, which the reference does not have)
  *   sage_vtiles()   <- v.to(torch.float16)            triton_impl.py:189
  *                      (fused with the attention's V tile layout)
+ *   sage_prepass_vt() <- both of the above in the pre-pass's launches
  *   sage_attn_fwd() <- _attn_fwd[grid](...) launch    triton_impl.py:186-199
  *                      _attn_fwd / _attn_fwd_inner    triton_impl.py:86-160
  *
@@ -47,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 4
+#define SAGE_ABI_VERSION 5
 
 /* element types (dtype codes used by every entry point) */
 #define SAGE_DTYPE_F32 0
@@ -131,6 +132,29 @@ int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int6
 int sage_vtiles(const void* v, int in_dtype, int64_t B, int64_t Hkv, int64_t Nkv, int64_t D,
                 const int64_t* v_strides, int pv_mode, const float* v_scale, void* out,
                 size_t out_bytes, void* stream);
+
+/*
+ * sage_prepass and sage_vtiles in one call (per_block_int8 and the
+ * v.to(torch.float16) before the attention launch, triton_impl.py:35-82, 189):
+ * the V tiles are written by the pre-pass's own launches — beside the K
+ * statistics for fp16/bf16 P.V, beside the K quantization for FP8 P.V (whose
+ * codes need v_scale, so v_mode must then be FP8 or FP8_SCALE).  The
+ * outputs equal those of sage_prepass followed by sage_vtiles(v, in_dtype,
+ * B, Hkv, Nkv, D, v_strides, pv_mode, v_scale, vtiles, vtile_bytes).
+ *
+ *  every argument of sage_prepass, then
+ *  pv_mode      SAGE_PV_F16 / SAGE_PV_BF16 / SAGE_PV_FP8, as sage_vtiles
+ *  vtiles       sage_vtile_bytes(B, Hkv, Nkv, D, pv_mode) bytes (vtile_bytes);
+ *               v and v_strides are required
+ */
+int sage_prepass_vt(const void* q, const void* k, const void* v, int in_dtype, int64_t B, int64_t Hq,
+                    int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, const int64_t* q_strides,
+                    const int64_t* k_strides, const int64_t* v_strides, float q_mul, int blkq,
+                    int blkk, int q_sub, int smooth_k, int v_mode, int8_t* q8,
+                    const int64_t* q8_strides, float* q_scale, int8_t* k8, const int64_t* k8_strides,
+                    float* k_scale, float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                    void* workspace, size_t workspace_bytes, int pv_mode, void* vtiles,
+                    size_t vtile_bytes, void* stream);
 
 /*
  * Fused attention: O = softmax2(dequant(Q8 K8^T)) V with an online,

@@ -25,8 +25,8 @@ def lib(hip_impl):
 
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_attn_fwd_q", "sage_flash_fwd",
-                                     "sage_last_error", "sage_prepass", "sage_prepass_workspace_bytes",
-                                     "sage_vtile_bytes", "sage_vtiles"]
+                                     "sage_last_error", "sage_prepass", "sage_prepass_vt",
+                                     "sage_prepass_workspace_bytes", "sage_vtile_bytes", "sage_vtiles"]
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -75,6 +75,27 @@ def test_prepass_rejects_bad_arguments(lib, over, needle):
     rc = lib.sage_prepass(*_prepass_args(**over))
     msg = lib.sage_last_error().decode()
     assert rc != 0 and "invalid argument" in msg and needle in msg, msg
+
+
+@pytest.mark.parametrize("over,vt_over,needle", [
+    ({}, dict(pv=7), "pv_mode"),
+    ({}, dict(pv=2), "FP8 V tiles need v_mode"),          # FP8 tiles without v_scale
+    ({}, dict(vt=None), "null pointer"),
+    (dict(v=None), {}, "null V pointer"),
+    ({}, dict(vtb=1000), "vtiles"),                       # 1000 < 2*64*64*2 bytes
+    ({}, dict(vt=ctypes.c_void_p(24)), "aligned"),
+    (dict(q_sub=2), {}, "q_sub"),                         # the pre-pass's own checks still apply
+])
+def test_prepass_vt_rejects_bad_arguments(lib, over, vt_over, needle):
+    s3 = (ctypes.c_int64 * 3)(0, 0, 0)
+    base = dict(v=ctypes.c_void_p(16), vs=s3)
+    base.update(over)
+    tail = dict(pv=0, vt=ctypes.c_void_p(16), vtb=1 << 20, st=None)
+    tail.update(vt_over)
+    args = _prepass_args(**base)[:-1] + list(tail.values())
+    rc = lib.sage_prepass_vt(*args)
+    msg = lib.sage_last_error().decode()
+    assert rc != 0 and "invalid argument" in msg and needle in msg and "sage_prepass_vt" in msg, msg
 
 
 def test_attn_rejects_bad_arguments(lib):

@@ -11,6 +11,9 @@
 //        Q quant:       per (128-row block, head, batch) INT8 + scale(s)
 //        K quant:       here as well when no K statistics are needed
 //   B  K quant with the channel mean subtracted (+ FP8 V quant)
+// and, through sage_prepass_vt, the V tiles of sage_vtiles: in launch A with
+// fp16/bf16 P.V (they need nothing from the statistics), in launch B with
+// FP8 P.V (their codes need v_scale).
 //
 // Every block is 256 threads.  A block's data is read once from HBM with
 // 16-byte loads, held in registers while the block's max|x| is reduced, then
@@ -19,6 +22,7 @@
 #include <type_traits>
 
 #include "sage_device.h"
+#include "sage_vtile_dev.h"
 
 namespace sage {
 
@@ -48,7 +52,36 @@ struct PrepassArgs {
   int64_t nqb, nkb;  // blocks per head
   int64_t n_stat, n_qblk_a, n_kblk_a;  // role counts of launch A
   int64_t n_kblk_b, n_qblk_b;          // role counts of launch B (K blocks first)
+  uint8_t* vt;                         // V tiles (sage_prepass_vt), else NULL
+  int pv_mode;                         // their type
+  int64_t ntile;                       // 64-key tiles per head
+  int64_t n_vt_a, n_vt_b;              // V tile roles of launch A / B (last in each)
 };
+
+// The V tile role r (tile, head, batch) in a block of this pre-pass; vs_s
+// holds v_scale for FP8 (visible to every thread), pool >= the role's LDS.
+template <typename T, int D>
+__device__ __forceinline__ void vtile_role(const PrepassArgs& a, int64_t r, const float* vs_s, char* pool) {
+  const int64_t t = r % a.ntile, h = (r / a.ntile) % a.Hkv, b = r / (a.ntile * a.Hkv);
+  const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1];
+  const int64_t tile = (b * a.Hkv + h) * a.ntile + t;
+  switch (a.pv_mode) {
+    case SAGE_PV_F16:
+      vtile_block<T, D, SAGE_PV_F16>(src, a.sv[2], a.Nkv, t, vs_s, a.vt + tile * D * 64 * 2, pool);
+      break;
+    case SAGE_PV_BF16:
+      vtile_block<T, D, SAGE_PV_BF16>(src, a.sv[2], a.Nkv, t, vs_s, a.vt + tile * D * 64 * 2, pool);
+      break;
+    default:
+      vtile_block<T, D, SAGE_PV_FP8>(src, a.sv[2], a.Nkv, t, vs_s, a.vt + tile * D * 64, pool);
+      break;
+  }
+}
+
+template <int D>
+constexpr int vtile_pool_bytes() {
+  return vtile_lds_bytes<D, SAGE_PV_F16>();  // the largest of the three types
+}
 
 
 // ---------------------------------------------------------------------------
@@ -195,7 +228,8 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
 
 // ---------------------------------------------------------------------------
 // K statistics of one chunk [n0, n1): fp32 channel sums in the fixed order of
-// sage_quant_math.h, and (if vsrc) channel max|v|.
+// sage_quant_math.h (if psum: K smoothing), and (if vsrc) channel max|v|.
+// At least one of psum and vsrc is non-null.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __device__ __forceinline__ void kstats_chunk(const T* __restrict__ ksrc, int64_t ksn, const T* __restrict__ vsrc,
@@ -252,7 +286,7 @@ __device__ __forceinline__ void kstats_chunk(const T* __restrict__ ksrc, int64_t
     }
     __syncthreads();
   }
-  if (tl == 0) {
+  if (psum && tl == 0) {  // (no K smoothing: FP8 V statistics only, no sums)
 #pragma unroll
     for (int e = 0; e < 8; ++e) psum[cg * 8 + e] = row[e];
   }
@@ -333,7 +367,10 @@ template <typename T, int D, int NIQ, int NIK>
 __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs a) {
   __shared__ uint32_t amax_s[16];
   __shared__ float scl_s[16], rcp_s[16];
-  __shared__ float red_s[kPrepassThreads / (D / 8) * D];
+  // one pool for the statistics' reduction rows or a V tile's transpose
+  constexpr int kRed = kPrepassThreads / (D / 8) * D * (int)sizeof(float);
+  __shared__ __attribute__((aligned(16))) char pool[kRed > vtile_pool_bytes<D>() ? kRed : vtile_pool_bytes<D>()];
+  float* red_s = reinterpret_cast<float*>(pool);
   int64_t r = blockIdx.x;
   if (r < a.n_stat) {
     const int64_t c = r % a.nch, h = (r / a.nch) % a.Hkv, b = r / (a.nch * a.Hkv);
@@ -341,7 +378,8 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs 
     const T* ks = static_cast<const T*>(a.k) + b * a.sk[0] + h * a.sk[1];
     const T* vs = a.v_fp8 ? static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1] : nullptr;
     const int64_t slot = ((b * a.Hkv + h) * a.nch + c) * D;
-    kstats_chunk<T, D>(ks, a.sk[2], vs, a.sv[2], n0, n1, a.psum + slot,
+    // psum is NULL without K smoothing (the workspace then holds the V maxima only)
+    kstats_chunk<T, D>(ks, a.sk[2], vs, a.sv[2], n0, n1, a.smooth_k ? a.psum + slot : nullptr,
                        a.v_fp8 ? a.pamax + slot : nullptr, red_s);
     return;
   }
@@ -351,46 +389,69 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs 
     return;
   }
   r -= a.n_qblk_a;
-  if (r < a.n_kblk_a) quant_k_role<T, D, NIK>(a, r, nullptr, amax_s, scl_s, rcp_s);
+  if (r < a.n_kblk_a) {
+    quant_k_role<T, D, NIK>(a, r, nullptr, amax_s, scl_s, rcp_s);
+    return;
+  }
+  r -= a.n_kblk_a;
+  if (r < a.n_vt_a) vtile_role<T, D>(a, r, nullptr, pool);  // fp16 / bf16 tiles
 }
 
+// Channel mean of K (km_s) and FP8 V scale (vs_s) of one (batch, head) from
+// launch A's per-chunk partials, into LDS (threads < D); the K block 0 role
+// also writes them out.
+template <int D>
+__device__ __forceinline__ void head_stats(const PrepassArgs& a, int64_t b, int64_t h, bool write_out,
+                                           float* km_s, float* vs_s) {
+  const int tid = threadIdx.x;
+  const int64_t base = (b * a.Hkv + h) * a.nch * D;
+  if (tid >= D) return;
+  if (a.smooth_k && km_s) {
+    // issue every partial load first (nch <= 16), then add left to right
+    float part[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c) part[c] = c < a.nch ? a.psum[base + c * D + tid] : 0.0f;
+    float s = part[0];
+#pragma unroll
+    for (int c = 1; c < 16; ++c)
+      if (c < a.nch) s = s + part[c];
+    const float m = s / (float)a.Nkv;
+    km_s[tid] = m;
+    if (write_out) a.km[(b * a.Hkv + h) * D + tid] = m;
+  }
+  if (a.v_fp8) {
+    float m = a.pamax[base + tid];
+#pragma unroll
+    for (int c = 1; c < 16; ++c)
+      if (c < a.nch) m = fmaxf(m, a.pamax[base + c * D + tid]);
+    const float sc = m / 448.0f;
+    vs_s[tid] = sc;
+    if (write_out) a.v_scale[(b * a.Hkv + h) * D + tid] = sc;
+  }
+}
+
+// Roles: K blocks, then Q blocks, then (FP8 P.V) V tiles.
 template <typename T, int D, int NIQ, int NIK>
 __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs a) {
   __shared__ uint32_t amax_s[16];
   __shared__ float scl_s[16], rcp_s[16];
   __shared__ float km_s[D], vs_s[D];
-  const int64_t r = blockIdx.x;
-  if (r >= a.n_kblk_b) {  // Q blocks follow the K blocks
+  __shared__ __attribute__((aligned(16))) char pool[vtile_pool_bytes<D>()];
+  int64_t r = blockIdx.x;
+  if (r >= a.n_kblk_b + a.n_qblk_b) {
+    r -= a.n_kblk_b + a.n_qblk_b;
+    const int64_t h = (r / a.ntile) % a.Hkv, b = r / (a.ntile * a.Hkv);
+    head_stats<D>(a, b, h, false, nullptr, vs_s);
+    __syncthreads();
+    vtile_role<T, D>(a, r, vs_s, pool);
+    return;
+  }
+  if (r >= a.n_kblk_b) {
     quant_q_role<T, D, NIQ>(a, r - a.n_kblk_b, amax_s, scl_s, rcp_s);
     return;
   }
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
-  const int tid = threadIdx.x;
-  const int64_t base = (b * a.Hkv + h) * a.nch * D;
-  if (tid < D) {
-    if (a.smooth_k) {
-      // issue every partial load first (nch <= 16), then add left to right
-      float part[16];
-#pragma unroll
-      for (int c = 0; c < 16; ++c) part[c] = c < a.nch ? a.psum[base + c * D + tid] : 0.0f;
-      float s = part[0];
-#pragma unroll
-      for (int c = 1; c < 16; ++c)
-        if (c < a.nch) s = s + part[c];
-      const float m = s / (float)a.Nkv;
-      km_s[tid] = m;
-      if (kb == 0) a.km[(b * a.Hkv + h) * D + tid] = m;
-    }
-    if (a.v_fp8) {
-      float m = a.pamax[base + tid];
-#pragma unroll
-      for (int c = 1; c < 16; ++c)
-        if (c < a.nch) m = fmaxf(m, a.pamax[base + c * D + tid]);
-      const float s = m / 448.0f;
-      vs_s[tid] = s;
-      if (kb == 0) a.v_scale[(b * a.Hkv + h) * D + tid] = s;
-    }
-  }
+  head_stats<D>(a, b, h, kb == 0, km_s, vs_s);
   __syncthreads();
   quant_k_role<T, D, NIK>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
   if (a.v_rows) {
@@ -404,13 +465,13 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs 
 
 template <typename T, int D, int NIQ, int NIK>
 static int launch_prepass_ni(const PrepassArgs& a, hipStream_t st) {
-  const int64_t na = a.n_stat + a.n_qblk_a + a.n_kblk_a;
+  const int64_t na = a.n_stat + a.n_qblk_a + a.n_kblk_a + a.n_vt_a;
   if (na > 0) {
     hipLaunchKernelGGL((prepass_a_kernel<T, D, NIQ, NIK>), dim3((unsigned)na), dim3(kPrepassThreads), 0, st, a);
     if (int rc = check_launch("sage_prepass (launch A)")) return rc;
   }
   if (a.n_kblk_b > 0) {
-    const int64_t nb = a.n_kblk_b + a.n_qblk_b;
+    const int64_t nb = a.n_kblk_b + a.n_qblk_b + a.n_vt_b;
     hipLaunchKernelGGL((prepass_b_kernel<T, D, NIQ, NIK>), dim3((unsigned)nb), dim3(kPrepassThreads), 0, st, a);
     if (int rc = check_launch("sage_prepass (launch B)")) return rc;
   }
@@ -446,51 +507,60 @@ extern "C" size_t sage_prepass_workspace_bytes(int64_t B, int64_t Hkv, int64_t N
   return bytes;
 }
 
-extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
-                            int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
-                            const int64_t* q_strides, const int64_t* k_strides,
-                            const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
-                            int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
-                            float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
-                            float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
-                            void* workspace, size_t workspace_bytes, void* stream) {
+static int prepass_impl(const char* who, const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                        int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D, const int64_t* q_strides,
+                        const int64_t* k_strides, const int64_t* v_strides, float q_mul, int blkq, int blkk,
+                        int q_sub, int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides, float* q_scale,
+                        int8_t* k8, const int64_t* k8_strides, float* k_scale, float* km, uint8_t* v8,
+                        const int64_t* v8_strides, float* v_scale, void* workspace, size_t workspace_bytes,
+                        int pv_mode, void* vt, size_t vt_bytes, void* stream) {
   if (B <= 0 || Hq <= 0 || Hkv <= 0 || Nq <= 0 || Nkv <= 0)
-    return fail("sage_prepass: invalid argument: empty shape B=%lld Hq=%lld Hkv=%lld Nq=%lld Nkv=%lld",
-                (long long)B, (long long)Hq, (long long)Hkv, (long long)Nq, (long long)Nkv);
+    return fail("%s: invalid argument: empty shape B=%lld Hq=%lld Hkv=%lld Nq=%lld Nkv=%lld", who, (long long)B, (long long)Hq, (long long)Hkv, (long long)Nq, (long long)Nkv);
   if (D != 64 && D != 128)
-    return fail("sage_prepass: invalid argument: head_dim %lld (supported: 64, 128)", (long long)D);
+    return fail("%s: invalid argument: head_dim %lld (supported: 64, 128)", who, (long long)D);
   if (Hq % Hkv != 0)
-    return fail("sage_prepass: invalid argument: Hq=%lld not a multiple of Hkv=%lld", (long long)Hq,
+    return fail("%s: invalid argument: Hq=%lld not a multiple of Hkv=%lld", who, (long long)Hq,
                 (long long)Hkv);
   if (in_dtype != SAGE_DTYPE_F32 && in_dtype != SAGE_DTYPE_F16 && in_dtype != SAGE_DTYPE_BF16)
-    return fail("sage_prepass: invalid argument: in_dtype %d", in_dtype);
+    return fail("%s: invalid argument: in_dtype %d", who, in_dtype);
   auto blk_ok = [](int b) { return b >= 16 && b <= 256 && b % 16 == 0; };
   if (!blk_ok(blkq) || !blk_ok(blkk))
-    return fail("sage_prepass: invalid argument: blkq=%d blkk=%d (16..256, multiples of 16)", blkq, blkk);
+    return fail("%s: invalid argument: blkq=%d blkk=%d (16..256, multiples of 16)", who, blkq, blkk);
   if (q_sub != 1 && (q_sub < 16 || q_sub % 16 != 0 || blkq % q_sub != 0 || blkq / q_sub > 16))
-    return fail("sage_prepass: invalid argument: q_sub=%d for blkq=%d", q_sub, blkq);
+    return fail("%s: invalid argument: q_sub=%d for blkq=%d", who, q_sub, blkq);
   if (v_mode != SAGE_V_NONE && v_mode != SAGE_V_FP8 && v_mode != SAGE_V_FP8_SCALE)
-    return fail("sage_prepass: invalid argument: v_mode %d", v_mode);
+    return fail("%s: invalid argument: v_mode %d", who, v_mode);
   const bool vfp8 = v_mode != SAGE_V_NONE;  // V statistics and v_scale
   const bool vrows = v_mode == SAGE_V_FP8;  // row-major codes as well
   // q, q8 and q_scale all NULL: K (and V) only -- Q is quantized by sage_attn_fwd_q
   const bool do_q = q || q8 || q_scale;
   if ((do_q && (!q || !q8 || !q_scale || !q_strides || !q8_strides)) || !k || !k8 || !k_scale || !k_strides ||
       !k8_strides)
-    return fail("sage_prepass: invalid argument: null pointer");
-  if (smooth_k && !km) return fail("sage_prepass: invalid argument: km is null with smooth_k");
+    return fail("%s: invalid argument: null pointer", who);
+  if (smooth_k && !km) return fail("%s: invalid argument: km is null with smooth_k", who);
   if (vfp8 && (!v || !v_scale || !v_strides || (vrows && (!v8 || !v8_strides))))
-    return fail("sage_prepass: invalid argument: null V pointer with v_mode %d", v_mode);
+    return fail("%s: invalid argument: null V pointer with v_mode %d", who, v_mode);
   const int es = in_dtype == SAGE_DTYPE_F32 ? 4 : 2;
   if ((do_q && (!strides_ok(q_strides, es) || !strides_ok(q8_strides, 1))) || !strides_ok(k_strides, es) ||
       !strides_ok(k8_strides, 1) || (vfp8 && !strides_ok(v_strides, es)) || (vrows && !strides_ok(v8_strides, 1)))
-    return fail("sage_prepass: invalid argument: strides must keep 16-byte aligned rows");
+    return fail("%s: invalid argument: strides must keep 16-byte aligned rows", who);
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)q8 | (uintptr_t)k8 | (uintptr_t)(vfp8 ? v : nullptr) |
        (uintptr_t)(vrows ? v8 : nullptr)) % 16 != 0)
-    return fail("sage_prepass: invalid argument: base pointers must be 16-byte aligned");
+    return fail("%s: invalid argument: base pointers must be 16-byte aligned", who);
+  if (vt) {  // V tiles (sage_prepass_vt)
+    if (pv_mode != SAGE_PV_F16 && pv_mode != SAGE_PV_BF16 && pv_mode != SAGE_PV_FP8)
+      return fail("%s: invalid argument: pv_mode %d", who, pv_mode);
+    if (pv_mode == SAGE_PV_FP8 && !vfp8)
+      return fail("%s: invalid argument: FP8 V tiles need v_mode FP8 or FP8_SCALE (v_scale)", who);
+    if (!v || !v_strides) return fail("%s: invalid argument: null V pointer for the V tiles", who);
+    if (!strides_ok(v_strides, es) || (uintptr_t)v % 16 != 0 || (uintptr_t)vt % 16 != 0)
+      return fail("%s: invalid argument: V rows and the V tiles must be 16-byte aligned", who);
+    const size_t vneed = sage_vtile_bytes(B, Hkv, Nkv, D, pv_mode);
+    if (vt_bytes < vneed) return fail("%s: invalid argument: vtiles %zu bytes < %zu", who, vt_bytes, vneed);
+  }
   const size_t need = sage_prepass_workspace_bytes(B, Hkv, Nkv, D, smooth_k, v_mode);
   if (need > 0 && (!workspace || workspace_bytes < need))
-    return fail("sage_prepass: invalid argument: workspace %zu bytes < %zu", workspace_bytes, need);
+    return fail("%s: invalid argument: workspace %zu bytes < %zu", who, workspace_bytes, need);
 
   PrepassArgs a{};
   a.q = q;
@@ -506,7 +576,7 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
     a.sk[i] = k_strides[i];
     a.sq8[i] = do_q ? q8_strides[i] : 0;
     a.sk8[i] = k8_strides[i];
-    a.sv[i] = vfp8 ? v_strides[i] : 0;
+    a.sv[i] = vfp8 || vt ? v_strides[i] : 0;
     a.sv8[i] = vrows ? v8_strides[i] : 0;
   }
   a.q_mul = q_mul;
@@ -540,8 +610,14 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
   a.n_kblk_a = need_b ? 0 : a.nkb * Hkv * B;
   a.n_kblk_b = need_b ? a.nkb * Hkv * B : 0;
   a.n_qblk_b = need_b && do_q ? a.nqb * Hq * B : 0;
-  if (a.n_stat + a.n_qblk_a + a.n_kblk_a > 0x7FFFFFFF || a.n_kblk_b + a.n_qblk_b > 0x7FFFFFFF)
-    return fail("sage_prepass: invalid argument: grid too large");
+  // V tiles last in their launch: A for fp16/bf16, B for FP8 (v_scale)
+  a.vt = static_cast<uint8_t*>(vt);
+  a.pv_mode = pv_mode;
+  a.ntile = (Nkv + 63) / 64;
+  a.n_vt_a = vt && pv_mode != SAGE_PV_FP8 ? a.ntile * Hkv * B : 0;
+  a.n_vt_b = vt && pv_mode == SAGE_PV_FP8 ? a.ntile * Hkv * B : 0;
+  if (a.n_stat + a.n_qblk_a + a.n_kblk_a + a.n_vt_a > 0x7FFFFFFF || a.n_kblk_b + a.n_qblk_b + a.n_vt_b > 0x7FFFFFFF)
+    return fail("%s: invalid argument: grid too large", who);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
@@ -552,4 +628,33 @@ extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_
     default:
       return D == 64 ? launch_prepass<__bf16, 64>(a, st) : launch_prepass<__bf16, 128>(a, st);
   }
+}
+
+extern "C" int sage_prepass(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                            int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
+                            int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
+                            float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
+                            float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  return prepass_impl("sage_prepass", q, k, v, in_dtype, B, Hq, Hkv, Nq, Nkv, D, q_strides, k_strides, v_strides,
+                      q_mul, blkq, blkk, q_sub, smooth_k, v_mode, q8, q8_strides, q_scale, k8, k8_strides, k_scale,
+                      km, v8, v8_strides, v_scale, workspace, workspace_bytes, -1, nullptr, 0, stream);
+}
+
+extern "C" int sage_prepass_vt(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                               int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                               const int64_t* q_strides, const int64_t* k_strides,
+                               const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
+                               int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
+                               float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
+                               float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                               void* workspace, size_t workspace_bytes, int pv_mode, void* vtiles,
+                               size_t vtile_bytes, void* stream) {
+  if (!vtiles) return fail("sage_prepass_vt: invalid argument: null pointer (vtiles)");
+  return prepass_impl("sage_prepass_vt", q, k, v, in_dtype, B, Hq, Hkv, Nq, Nkv, D, q_strides, k_strides,
+                      v_strides, q_mul, blkq, blkk, q_sub, smooth_k, v_mode, q8, q8_strides, q_scale, k8,
+                      k8_strides, k_scale, km, v8, v8_strides, v_scale, workspace, workspace_bytes, pv_mode, vtiles,
+                      vtile_bytes, stream);
 }

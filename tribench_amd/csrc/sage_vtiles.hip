@@ -6,19 +6,12 @@
 // kernel copies each tile into LDS with direct (global -> LDS) loads and
 // reads every P.V operand as whole 16-byte chunks.
 //
-// Tile layout (element size EB: 2 for fp16/bf16, 1 for e4m3):
-//   byte of (b, h, key n, channel d) =
-//     ((((b*Hkv + h)*T + n/64)*D + d)*64 + pos(n % 64)) * EB,   T = ceil(Nkv/64)
-//   pos(32t + 8i + 4h + r) = 32h + 16t + 4i + r
-// pos() is the order in which lane half h of a 32x32 MFMA C tile holds the
-// keys of its column (registers 4i + r of key tiles t = 0, 1).  Keys past Nkv
-// hold 0.  e4m3 codes are RNE_sat(v / v_scale[d]) (0 where v_scale[d] == 0),
-// the same codes as the pre-pass's row-major FP8 V.
-//
-// One block per tile: 256 threads load the 64 x D tile with 16-byte loads
-// along the rows, convert, transpose through LDS and store 16-byte chunks.
-// Build with -ffp-contract=off (the e4m3 division must be IEEE).
-#include "sage_device.h"
+// The tile layout and the per-tile work are in sage_vtile_dev.h (shared with
+// the pre-pass): one block per tile, 256 threads load the 64 x D tile with
+// 16-byte loads along the rows, convert, transpose through LDS and store
+// 16-byte chunks.  Build with -ffp-contract=off (the e4m3 division must be
+// IEEE).
+#include "sage_vtile_dev.h"
 
 namespace sage {
 
@@ -30,66 +23,20 @@ struct VtileArgs {
   uint8_t* out;
 };
 
-__device__ __forceinline__ int vtile_pos(int k) {
-  return ((k >> 2) & 1) * 32 + (k >> 5) * 16 + ((k >> 3) & 3) * 4 + (k & 3);
-}
-
-template <int PVM>
-__device__ __forceinline__ uint16_t to16(float x);
-template <>
-__device__ __forceinline__ uint16_t to16<SAGE_PV_F16>(float x) {
-  return __builtin_bit_cast(uint16_t, (_Float16)x);
-}
-template <>
-__device__ __forceinline__ uint16_t to16<SAGE_PV_BF16>(float x) {
-  return __builtin_bit_cast(uint16_t, (__bf16)x);
-}
-
 template <typename T, int D, int PVM>
 __global__ __launch_bounds__(256) void vtile_kernel(VtileArgs a) {
-  constexpr bool kF8 = PVM == SAGE_PV_FP8;
-  constexpr int EB = kF8 ? 1 : 2;
-  constexpr int RP = 64 * EB + 4;  // LDS row pitch: an odd number of dwords
-  constexpr int CG = D / 8;        // 8-channel groups per key row
-  constexpr int NIT = 64 * CG / 256;
-  __shared__ __attribute__((aligned(16))) char tile_s[D * RP];
+  __shared__ __attribute__((aligned(16))) char tile_s[vtile_lds_bytes<D, PVM>()];
   __shared__ float vs_s[D];
   const int64_t r = blockIdx.x;
   const int64_t t = r % a.ntile, h = (r / a.ntile) % a.Hkv, b = r / (a.ntile * a.Hkv);
-  const int tid = threadIdx.x;
-  const int64_t k0 = t * 64;
-  const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1];
-  if constexpr (kF8) {
-    if (tid < D) vs_s[tid] = a.v_scale[(b * a.Hkv + h) * D + tid];
+  if constexpr (PVM == SAGE_PV_FP8) {
+    if (threadIdx.x < D) vs_s[threadIdx.x] = a.v_scale[(b * a.Hkv + h) * D + threadIdx.x];
     __syncthreads();
   }
-#pragma unroll
-  for (int i = 0; i < NIT; ++i) {
-    const int it = tid + 256 * i;
-    const int cg = it % CG, key = it / CG;
-    const int64_t n = k0 + key;
-    const Raw8<T> x = n < a.Nkv ? load8<T>(src + n * a.sv[2] + 8 * cg) : zero8<T>();
-    const int pos = vtile_pos(key);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int d = 8 * cg + e;
-      const float val = elem<T>(x, e);
-      if constexpr (kF8) {
-        const float s = vs_s[d];
-        *reinterpret_cast<uint8_t*>(tile_s + d * RP + pos) = f32_to_e4m3(s > 0.0f ? val / s : 0.0f);
-      } else {
-        *reinterpret_cast<uint16_t*>(tile_s + d * RP + 2 * pos) = to16<PVM>(val);
-      }
-    }
-  }
-  __syncthreads();
-  constexpr int CPR = 4 * EB;  // 16-byte chunks per tile row
+  constexpr int EB = PVM == SAGE_PV_FP8 ? 1 : 2;
+  const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1];
   uint8_t* dst = a.out + ((b * a.Hkv + h) * a.ntile + t) * (int64_t)D * 64 * EB;
-  for (int it = tid; it < D * CPR; it += 256) {
-    const int d = it / CPR, c = it % CPR;
-    const uint32_t* s4 = reinterpret_cast<const uint32_t*>(tile_s + d * RP + 16 * c);
-    *reinterpret_cast<uint4*>(dst + (int64_t)d * 64 * EB + 16 * c) = make_uint4(s4[0], s4[1], s4[2], s4[3]);
-  }
+  vtile_block<T, D, PVM>(src, a.sv[2], a.Nkv, t, vs_s, dst, tile_s);
 }
 
 template <typename T, int PVM>

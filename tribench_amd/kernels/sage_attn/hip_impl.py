@@ -7,9 +7,10 @@ buffer with torch on the inputs' device and calls the C ABI of
 ``libsage_attn.so`` (include/sage_attn.h) through ctypes, on torch's current
 stream:
 
-    sage_prepass   per_block_int8 (triton_impl.py:35-82) + K smoothing (+ FP8 V scales)
-    sage_vtiles    v.to(torch.float16) (triton_impl.py:189), in the attention's V tile layout
-    sage_attn_fwd  _attn_fwd launch (triton_impl.py:186-199)
+    sage_prepass     per_block_int8 (triton_impl.py:35-82) + K smoothing (+ FP8 V scales)
+    sage_vtiles      v.to(torch.float16) (triton_impl.py:189), in the attention's V tile layout
+    sage_prepass_vt  both, in the pre-pass's launches (what run() uses)
+    sage_attn_fwd    _attn_fwd launch (triton_impl.py:186-199); sage_attn_fwd_q quantizes Q itself
 
 There is no CPU or PyTorch fallback: without a ROCm device or without the
 library the call raises.  The module is loaded by file path (no parent
@@ -26,7 +27,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
 # rows per Q scale for each q_gran: one block of 128 rows (the reference), one
@@ -78,6 +79,8 @@ def _load():
         vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, p64, p64, p64, f32, i32, i32, i32, i32, i32,
         vp, p64, vp, vp, p64, vp, vp, vp, p64, vp, vp, sz, vp,
     ]
+    lib.sage_prepass_vt.restype = i32
+    lib.sage_prepass_vt.argtypes = lib.sage_prepass.argtypes[:-1] + [i32, vp, sz, vp]
     lib.sage_vtile_bytes.restype = sz
     lib.sage_vtile_bytes.argtypes = [i64, i64, i64, i64, i32]
     lib.sage_vtiles.restype = i32
@@ -218,8 +221,8 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         v8 = _empty_like_layout(v, torch.uint8)
     ws_bytes = lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), v_mode)
     ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
-    uses_v = v_mode != V_NONE
-    rc = lib.sage_prepass(
+    uses_v = v_mode != V_NONE or pv_dtype is not None
+    args = [
         _ptr(q) if quant_q else None, _ptr(k), _ptr(v) if uses_v else None, _TORCH_CODES[q.dtype], B, Hq, Hkv,
         Nq, Nkv, D, _strides(q, tensor_layout) if quant_q else None, _strides(k, tensor_layout),
         _strides(v, tensor_layout) if uses_v else None,
@@ -227,9 +230,18 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         _ptr(q8), _strides(q8, tensor_layout) if quant_q else None, _ptr(q_scale), _ptr(k8),
         _strides(k8, tensor_layout),
         _ptr(k_scale), _ptr(km), _ptr(v8), _strides(v8, tensor_layout) if v_fp8 else None, _ptr(v_scale),
-        _ptr(ws), ctypes.c_size_t(ws_bytes), _stream(dev),
-    )
-    _check(rc, "sage_prepass")
+        _ptr(ws), ctypes.c_size_t(ws_bytes),
+    ]
+    vt = None
+    if pv_dtype is None:
+        rc = lib.sage_prepass(*args, _stream(dev))
+        _check(rc, "sage_prepass")
+    else:
+        # the V tiles of vtiles(), written by the pre-pass's own launches
+        nbytes = lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype])
+        vt = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
+        rc = lib.sage_prepass_vt(*args, PV_MODES[pv_dtype], _ptr(vt), ctypes.c_size_t(nbytes), _stream(dev))
+        _check(rc, "sage_prepass_vt")
     out = {"k8": k8, "k_scale": k_scale, "workspace": ws}
     if quant_q:
         out["q8"] = q8
@@ -240,8 +252,8 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         out["v8"] = v8
     if v_scale is not None:
         out["v_scale"] = v_scale
-    if pv_dtype is not None:
-        out["vt"] = vtiles(v, pv_dtype, v_scale, tensor_layout=tensor_layout)
+    if vt is not None:
+        out["vt"] = vt
     return out
 
 
