@@ -1,6 +1,8 @@
 """Benchmark of the sage_attn hot path on one MI355X (driver contract).
 
-One step = one SageAttention forward (HIP pre-pass + fused attention) over the
+One step = one SageAttention forward (HIP pre-pass + fused attention; Q is
+quantized where hip_impl.run puts it, in the attention kernel's prologue at
+D = 128, see --q-quant) over the
 BASELINE.json configuration 2 workload with the inputs already resident in
 HBM:  B=4, H=32, N=4096, D=128, bf16, non-causal, K channel offset ~N(0,2),
 INT8 Q/K per block (BLKQ 128, BLKK 64), fp16 P.V, fp32 accumulation.
@@ -13,7 +15,7 @@ SDPA (a restatement of reference.py:ref) on a bounded sample of the same
 workload on this host's cores.
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
-                  [--no-cpu-baseline] [--copy-probe-gib G] [--fused-q]
+                  [--no-cpu-baseline] [--copy-probe-gib G] [--q-quant auto|prologue|pre-pass]
 """
 from __future__ import annotations
 
@@ -110,8 +112,9 @@ def main(argv=None) -> int:
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
-    ap.add_argument("--fused-q", action="store_true",
-                    help="quantize Q in the attention kernel's prologue instead of in the pre-pass")
+    ap.add_argument("--q-quant", default="auto", choices=["auto", "prologue", "pre-pass"],
+                    help="where Q is quantized: as hip_impl.run does by default (auto), in the attention "
+                         "kernel's prologue, or in the pre-pass")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="first run one plain device copy of this many GiB (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count)")
@@ -149,14 +152,15 @@ def main(argv=None) -> int:
 
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream(dev)
+    fused_q = H.fuse_q_default(D) if args.q_quant == "auto" else args.q_quant == "prologue"
 
     def step(ev=None):
         if ev is not None:
             ev[0].record(stream)
-        pre = H.prepass(q, k, v, q_sub=q_sub, smooth_k=True, pv_dtype=pv, quant_q=not args.fused_q)
+        pre = H.prepass(q, k, v, q_sub=q_sub, smooth_k=True, pv_dtype=pv, quant_q=not fused_q)
         if ev is not None:
             ev[1].record(stream)
-        if args.fused_q:
+        if fused_q:
             H.attention_q(q, k, v, pre, causal, pv_dtype=pv, q_sub=q_sub, out=out)
         else:
             H.attention(q, k, v, pre, causal, pv_dtype=pv, q_sub=q_sub, out=out)
@@ -182,8 +186,8 @@ def main(argv=None) -> int:
     step_ms = np.array([e[0].elapsed_time(e[2]) for e in evs])
 
     value = metric_ops / (ms * 1e-3) / 1e12
-    # Q (not with --fused-q) and K quantization + V tiles
-    pre_bytes = est["prepass_bytes_k" if args.fused_q else "prepass_bytes"] + est["vtile_bytes"]
+    # Q (unless the attention kernel quantizes it) and K quantization + V tiles
+    pre_bytes = est["prepass_bytes_k" if fused_q else "prepass_bytes"] + est["vtile_bytes"]
     achieved = algo_ops / (float(attn_ms.mean()) * 1e-3) / 1e12
     res = {
         "metric": "sage_attn effective TOPS (4*B*H*N^2*D/t)",
@@ -201,7 +205,7 @@ def main(argv=None) -> int:
         "config": {"workload": f"{args.config}: {case['desc']}", "batch": B, "heads": Hq,
                    "kv_heads": k.shape[1], "seq_len": N, "head_dim": D, "causal": causal, "pv_dtype": pv,
                    "q_gran": case.get("q_gran", "block"), "smooth_k": True,
-                   "q_quant": "attention prologue" if args.fused_q else "pre-pass"},
+                   "q_quant": "attention prologue" if fused_q else "pre-pass"},
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
         "latency_ms": {"p50": round(float(np.percentile(step_ms, 50)), 4),
                        "p95": round(float(np.percentile(step_ms, 95)), 4)},

@@ -602,15 +602,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       }
       qsc = block_scale(am);
       const float rc = qsc > 0.0f ? 1.0f / qsc : 0.0f;
-      const bool fast = fast_div_ok(qsc);
+      // one wave-uniform choice of the division (a per-lane flag would put a
+      // branch around every element)
+      auto quantize_regs = [&](auto fast_tag) __attribute__((always_inline)) {
+        constexpr bool kFast = decltype(fast_tag)::value;
 #pragma unroll
-      for (int c = 0; c < KC; ++c) {
-        int w[4] = {0, 0, 0, 0};
+        for (int c = 0; c < KC; ++c) {
+          int w[4] = {0, 0, 0, 0};
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          w[e >> 2] |= (int)(uint32_t)(uint8_t)quant_elem(xq[c][e], qsc, rc, fast) << (8 * (e & 3));
-        qreg[c] = (v4i){w[0], w[1], w[2], w[3]};
-        if (a.q8_out && valid)
+          for (int e = 0; e < 16; ++e)
+            w[e >> 2] |= (int)(uint32_t)(uint8_t)quant_elem(xq[c][e], qsc, rc, kFast) << (8 * (e & 3));
+          qreg[c] = (v4i){w[0], w[1], w[2], w[3]};
+        }
+      };
+      if (__builtin_amdgcn_ballot_w64(!fast_div_ok(qsc)) == 0) quantize_regs(std::true_type{});
+      else quantize_regs(std::false_type{});
+      if (a.q8_out && valid) {
+#pragma unroll
+        for (int c = 0; c < KC; ++c)
           *reinterpret_cast<v4i*>(a.q8_out + b * a.sq[0] + h * a.sq[1] + (int64_t)row * a.sqn + 32 * c + 16 * hh) =
               qreg[c];
       }

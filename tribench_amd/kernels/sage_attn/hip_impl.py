@@ -264,11 +264,21 @@ def q_sub_of(q_gran):
     return Q_GRAN_ROWS[q_gran]
 
 
+def fuse_q_default(head_dim):
+    """Where Q is quantized when the caller does not say: in the attention
+    kernel's prologue at D = 128 (measured 1-2 % faster per forward at
+    configurations 2 and 3, even at 5), in the pre-pass at D = 64 (the
+    prologue costs more than it saves there: 2 % slower at configuration 4)."""
+    return head_dim == 128
+
+
 def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
-                  fuse_q=False, tensor_layout="HND", **kw):
+                  fuse_q=None, tensor_layout="HND", **kw):
     """The pre-pass of :func:`run` alone, with run's arguments (the harness
     times it as the ``prepass`` stage to report its HBM rate)."""
     q_sub = q_sub_of(q_gran)
+    if fuse_q is None:
+        fuse_q = fuse_q_default(_dims(q, tensor_layout)[3])
     return prepass(q, k, v, sm_scale, q_sub=q_sub, smooth_k=smooth_k, pv_dtype=pv_dtype, quant_q=not fuse_q,
                    tensor_layout=tensor_layout)
 
@@ -347,7 +357,7 @@ def attention_q(q, k, v, pre, causal=False, sm_scale=None, *, pv_dtype="fp16", q
 
 
 def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
-        fuse_q=False, tensor_layout="HND", return_intermediates=False, **kw):
+        fuse_q=None, tensor_layout="HND", return_intermediates=False, **kw):
     """SageAttention forward on MI355X: INT8 QK^T, online softmax, P.V.
 
     Same call as run_sage_attn(q, k, v, causal=False, sm_scale=None)
@@ -361,15 +371,17 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
                32 rows (the attention kernel's per-wavefront tile); "thread":
                one per row (each lane of the kernel holds one query row)
     smooth_k   subtract the per-channel K mean before quantizing (default on)
-    fuse_q     quantize Q in the attention kernel's prologue instead of the
-               pre-pass (the same Q8 and scales; off by default: on MI355X the
-               prologue work costs about what the pre-pass saves)
+    fuse_q     quantize Q in the attention kernel's prologue (True) or in the
+               pre-pass (False): the same Q8 and scales bit for bit; by
+               default (None) as fuse_q_default(D) measured faster
     """
     if pv_dtype not in PV_MODES:
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
     q_sub = q_sub_of(q_gran)
     _check_inputs(q, k, v, tensor_layout)
     blkq, blkk = 128, 64  # BLOCK_M / BLOCK_N of triton_impl.py:166-167
+    if fuse_q is None:
+        fuse_q = fuse_q_default(_dims(q, tensor_layout)[3])
     pre = prepass(q, k, v, sm_scale, blkq=blkq, blkk=blkk, q_sub=q_sub, smooth_k=smooth_k,
                   pv_dtype=pv_dtype, quant_q=not fuse_q, tensor_layout=tensor_layout)
     if fuse_q:
