@@ -105,7 +105,7 @@ def test_attn_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
     assert torch.equal(o1, o2.transpose(1, 2))
 
 
-# Q quantized in the attention kernel's prologue (sage_attn_fwd_q, run's default)
+# Q quantized in the attention kernel's prologue (sage_attn_fwd_q, run's default at D = 128)
 # against the pre-pass path: the same Q8 and scales bit for bit (and the
 # oracle's), hence the same output bit for bit.
 # (B, Hq, Hkv, N, D, dtype, causal, q_gran, layout)
