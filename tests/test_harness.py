@@ -198,6 +198,35 @@ def test_tolerance_precedence():
     assert _get_tolerance("fp16", spec) == (1e-3, 5e-2)
 
 
+def test_per_case_tolerance_overrides():
+    spec = CorrectnessSpec(atol=5e-2, rtol=5e-2, per_dtype={"fp16": {"atol": 1e-3}},
+                           per_case={"wide": {"atol": 2.0, "min_cos": 0.999}})
+    assert spec.for_case("other") is spec and spec.for_case(None) is spec
+    wide = spec.for_case("wide")
+    assert (wide.atol, wide.rtol, wide.min_cos) == (2.0, 5e-2, 0.999)
+    assert _get_tolerance("fp16", wide) == (2.0, 5e-2)  # the case's atol beats the per-dtype one
+    ref = torch.randn(1000, generator=torch.Generator().manual_seed(1))
+    assert not check_correctness(ref, ref + 1.0, "bf16", spec).passed
+    assert check_correctness(ref, ref + 1.0 * (ref > 0), "bf16", spec.for_case("wide")).passed is False  # cosine
+    one_big = ref + 0.5 * (torch.arange(1000) == 7)  # one error of 0.5: inside atol 2, cosine ~ 1
+    assert check_correctness(ref, one_big, "bf16", spec.for_case("wide")).passed
+    assert not check_correctness(ref, one_big, "bf16", spec).passed
+    m = copy.deepcopy(VALID_META)
+    m["correctness"] = {"atol": 5e-2, "per_case": {"small": {"atol": 1.0}}}
+    assert validate_meta(m) == []
+    m["correctness"]["per_case"] = {"nope": {"atol": 1.0}}
+    assert any("unknown case" in e for e in validate_meta(m))
+    m["correctness"]["per_case"] = {"small": {"tol": 1.0}}
+    assert any("takes atol" in e for e in validate_meta(m))
+
+
+def test_sage_pack_fp8_case_gate():
+    meta = load_meta(Path(KernelRegistry().get_meta("sage_attn").kernel_dir) / "meta.json")
+    c5 = meta.correctness.for_case("cfg5_fp8pv_b1h32n32768d128")
+    assert (c5.atol, c5.rtol, c5.min_cos) == (2.0, 5e-2, 0.999)
+    assert meta.correctness.for_case("cfg2_b4h32n4096d128").atol == 5e-2
+
+
 def test_check_correctness_reports_cosine_and_bounds():
     ref = torch.randn(1000, generator=torch.Generator().manual_seed(0))
     res = check_correctness(ref, ref + 1e-3, "bf16", CorrectnessSpec(atol=5e-2, rtol=5e-2, max_abs=2e-2,

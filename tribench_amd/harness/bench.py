@@ -172,7 +172,7 @@ def run_benchmark(
         ref_out = reference_fn(**inputs)
         out = triton_fn(**inputs)
         _sync(device)
-        corr = check_correctness(ref_out, out, dtype_str, meta.correctness)
+        corr = check_correctness(ref_out, out, dtype_str, meta.correctness.for_case(case["case_name"]))
         del ref_out, out
 
     lats = timer(lambda: triton_fn(**inputs), warmup_ms, rep_ms)

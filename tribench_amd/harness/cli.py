@@ -157,7 +157,7 @@ def _cmd_test(args) -> int:
                 try:
                     out = fn(**inputs)
                     _sync(args.device)
-                    res = check_correctness(ref_out, out, case["dtype"], meta.correctness)
+                    res = check_correctness(ref_out, out, case["dtype"], meta.correctness.for_case(case["case_name"]))
                     status = "PASS" if res.passed else "FAIL"
                     cos = "" if res.cosine is None else f"  cos={res.cosine:.6f}"
                     print(f"    {status}  {case['case_name']} [{label}] dtype={case['dtype']}  "

@@ -3,7 +3,9 @@
 Same tolerance precedence and allclose test as correctness.py:14-106 of the
 reference; the result also carries the cosine similarity, and the pack may
 state north-star bounds (``max_abs``, ``min_cos`` in meta.json's
-``correctness``) that must hold as well.
+``correctness``) that must hold as well.  ``correctness.per_case`` may
+override any of the four for a named case (callers pass
+``spec.for_case(name)``).
 """
 from __future__ import annotations
 

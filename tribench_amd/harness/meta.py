@@ -55,6 +55,7 @@ def load_meta(path: str | Path) -> KernelMeta:
         per_dtype=corr.get("per_dtype", {}),
         max_abs=corr.get("max_abs"),
         min_cos=corr.get("min_cos"),
+        per_case=corr.get("per_case", {}),
     )
     return KernelMeta(
         schema_version=raw["schema_version"],
@@ -121,6 +122,16 @@ def validate_meta(raw: dict[str, Any]) -> list[str]:
                 errors.append(f"cases[{i}] missing 'name' field")
     elif cases is not None:
         errors.append("'cases' must be a list")
+    per_case = (raw.get("correctness") or {}).get("per_case", {})
+    if not isinstance(per_case, dict):
+        errors.append("'correctness.per_case' must be a dict")
+    else:
+        names = {c.get("name") for c in cases if isinstance(c, dict)} if isinstance(cases, list) else set()
+        for name, o in per_case.items():
+            if name not in names:
+                errors.append(f"correctness.per_case names unknown case '{name}'")
+            elif not isinstance(o, dict) or set(o) - {"atol", "rtol", "max_abs", "min_cos"}:
+                errors.append(f"correctness.per_case['{name}'] takes atol, rtol, max_abs, min_cos")
     return errors
 
 

@@ -45,6 +45,17 @@ class CorrectnessSpec:
     per_dtype: dict[str, dict[str, float]] = dc.field(default_factory=dict)
     max_abs: float | None = None
     min_cos: float | None = None
+    # case name -> overrides of atol / rtol / max_abs / min_cos for that case
+    per_case: dict[str, dict[str, float]] = dc.field(default_factory=dict)
+
+    def for_case(self, case_name: str | None) -> "CorrectnessSpec":
+        """This spec with the case's overrides applied (itself if it has none)."""
+        o = self.per_case.get(case_name or "", {})
+        if not o:
+            return self
+        return dc.replace(self, atol=o.get("atol", self.atol), rtol=o.get("rtol", self.rtol),
+                          per_dtype={} if ("atol" in o or "rtol" in o) else self.per_dtype,
+                          max_abs=o.get("max_abs", self.max_abs), min_cos=o.get("min_cos", self.min_cos))
 
 
 @dc.dataclass
