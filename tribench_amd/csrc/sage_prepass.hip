@@ -104,6 +104,12 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
   const int nsub = blk / q_sub;
 
   if (tid < 16) amax_s[tid] = 0u;
+  // the thread's 16 channels are the same in every item (256 % CPR == 0):
+  // their means go to registers once, not through LDS for every element
+  static_assert(kPrepassThreads % CPR == 0, "items of a thread share their channels");
+  float kmr[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) kmr[e] = km_s ? km_s[(tid % CPR) * 16 + e] : 0.0f;
   Raw8<T> raw[NI][2];
   float amx[NI];
 #pragma unroll
@@ -122,14 +128,14 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int it = tid + kPrepassThreads * j;
-    const int row = it / CPR, c = it % CPR;
+    const int row = it / CPR;
     float am = 0.0f;
     if (it < nit && row < rows_valid) {  // tail rows stay out of the block max
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         float x = elem<T>(raw[j][e >> 3], e & 7);
         if (use_mul) x = x * mul;
-        if (km_s) x = x - km_s[c * 16 + e];
+        if (km_s) x = x - kmr[e];
         am = fmaxf(am, fabsf(x));
       }
     }
@@ -160,7 +166,7 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
         for (int e = 0; e < 16; ++e) {
           float x = elem<T>(raw[j][e >> 3], e & 7);
           if (use_mul) x = x * mul;
-          if (km_s) x = x - km_s[c * 16 + e];
+          if (km_s) x = x - kmr[e];
           const int8_t qv = quant_elem(x, sc[j], rc[j], kFast);
           w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
         }
@@ -215,7 +221,7 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
       for (int e = 0; e < 16; ++e) {
         float x = elem<T>(raw[j][e >> 3], e & 7);
         if (use_mul) x = x * mul;
-        if (km_s) x = x - km_s[c * 16 + e];
+        if (km_s) x = x - kmr[e];
         const int8_t qv = quant_elem(x, sc, rc, kFast);
         w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
       }
