@@ -213,6 +213,52 @@ def test_attn_cross_lengths(case, hip_impl, gpu_device):
     assert max_abs <= bound and cos >= MIN_COS
 
 
+def rising_inputs(B, H, N, D, step, seed):
+    """q, k, v (fp32, HND) whose scores rise by about `step` log2 units per
+    64-key block: the queries share a direction u and the keys drift along it."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(D, generator=g)
+    u /= u.norm()
+    q = torch.randn(B, H, N, D, generator=g) + 4.0 * u
+    j = torch.arange(N, dtype=torch.float32)[None, None, :, None]
+    k = torch.randn(B, H, N, D, generator=g) + step * (j / 64.0) * D ** 0.5 / (4.0 * 1.4426950408889634) * u
+    return q, k, torch.randn(B, H, N, D, generator=g)
+
+
+# Scores rising from key block to key block (step 2.5: about a quarter of the
+# blocks move a row's running max by more than the lazy-rescale threshold of
+# 8, a third by more than 7).  In the mask-free loop the shortcut that forms P
+# against the running max then fails its bound and the block is redone, and
+# lazy O rescales happen throughout.  The keys' large values cost INT8
+# accuracy (the emulation itself is up to 4.7e-2 off SDPA here), so the
+# kernel is held to the emulation bound and SDPA to the cosine only.
+# (B, H, N, D, dtype, causal, pv, q_gran)
+RISING = [
+    (1, 2, 1000, 64, "fp16", True, "fp16", "block"),
+    (1, 2, 1000, 128, "bf16", False, "bf16", "block"),
+    (1, 2, 1000, 128, "bf16", False, "fp16", "thread"),
+    (1, 2, 777, 128, "fp32", True, "fp16", "wave"),
+]
+
+
+@pytest.mark.parametrize("case", RISING, ids=lambda c: f"N{c[2]}D{c[3]}-{c[4]}-c{int(c[5])}-pv{c[6]}-{c[7]}")
+def test_attn_rising_scores(case, hip_impl, gpu_device):
+    B, H, N, D, dtype, causal, pv, q_gran = case
+    print(f"[attn-rising] {case}", flush=True)
+    q, k, v = (t.to(DT[dtype]) for t in rising_inputs(B, H, N, D, 2.5, seed=N + D))
+    o, pre = hip_impl.run(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), causal=causal, pv_dtype=pv,
+                          q_gran=q_gran, return_intermediates=True)
+    torch.cuda.synchronize()
+    got = o.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    qf, kf, vf = (t.float().numpy() for t in (q, k, v))
+    emu = O.sage_emulate(pre["q8"].cpu().numpy(), pre["q_scale"].cpu().numpy(), pre["k8"].cpu().numpy(),
+                         pre["k_scale"].cpu().numpy(), vf, causal=causal, q_sub=hip_impl.q_sub_of(q_gran))
+    max_abs, cos = _metrics(got, O.sdpa(qf, kf, vf, causal=causal))
+    print(f"  vs emulation: {_vs_emulation(got, emu, q.dtype):.3e}; vs SDPA: max_abs={max_abs:.3e} cos={cos:.6f}")
+    assert _vs_emulation(got, emu, q.dtype) <= EMUL_ABS and cos >= MIN_COS
+
+
 # full-size configurations (BASELINE.json configs 2-4) against the fp32 reference on the GPU
 FULL = {
     "cfg2": dict(batch_size=4, num_heads=32, seq_len=4096, head_dim=128, k_offset_std=2.0, pv_dtype="fp16"),

@@ -109,6 +109,24 @@ def test_flash_small_vs_sdpa(case, flash, gpu_device):
     assert np.allclose(got, want, atol=ATOL, rtol=RTOL) and cos >= 0.9999
 
 
+@pytest.mark.parametrize("dtype,D,causal", [("fp16", 128, False), ("bf16", 64, True)])
+def test_flash_rising_scores(dtype, D, causal, flash, gpu_device):
+    """Scores rising by about 2.5 log2 units per 64-key block (the queries
+    share a direction the keys drift along): the running max moves again and
+    again, so the mask-free loop redoes blocks whose P exceed its shortcut's
+    bound and rescales O lazily throughout; the reference pack's gate holds."""
+    print(f"[flash-rising] {dtype} D={D} causal={causal}", flush=True)
+    from test_gpu_attn import rising_inputs
+    q, k, v = (t.to(DT[dtype]) for t in rising_inputs(1, 2, 1000, D, 2.5, seed=D))
+    o = flash.run(q.to(gpu_device), k.to(gpu_device), v.to(gpu_device), causal=causal)
+    torch.cuda.synchronize()
+    got = o.float().cpu().numpy().astype(np.float64)
+    want = O.sdpa(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal=causal)
+    cos = float((got * want).sum() / np.linalg.norm(got) / np.linalg.norm(want))
+    print(f"  max_abs={np.abs(got - want).max():.3e} cos={cos:.7f}")
+    assert np.allclose(got, want, atol=ATOL, rtol=RTOL) and cos >= 0.9999
+
+
 def test_flash_nhd_matches_hnd(flash, gpu_device):
     gen = torch.Generator().manual_seed(5)
     q, k, v = (torch.randn(2, 4, 333, 64, generator=gen).to(torch.bfloat16).to(gpu_device) for _ in range(3))

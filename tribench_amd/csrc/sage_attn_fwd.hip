@@ -519,6 +519,65 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lsum += ls[0] + ls[1];
     }
   };
+  // Mask-free block, row max not recomputed: P is formed against the running
+  // max m_use straight away.  softmax() keeps m_use too unless the block max
+  // exceeds it by more than kTau, that is unless some P exceeds
+  // 2^(kTau + kShift).  A lane's partial row sum bounds each of its P (sums
+  // of non-negative values, fp16 ones included, never fall below their
+  // largest term), so if every lane's sum is at most 2^(kTau + kShift - 1)
+  // the block max is within kTau of m_use and P and the new lsum are the
+  // ones softmax() computes, bit for bit; nothing else changes.  The margin
+  // covers the rounding of the INT8 bias (error below 0.75 * c, so the
+  // shortcut is exact for c < 4/3); an m_use of -inf (sums of +inf) and NaN
+  // scores fail the test.  Otherwise softmax() redoes the block from the
+  // untouched S.  Not used for FP8 P: with kShift = 6 the sums of a typical
+  // block exceed the bound.
+  auto softmax_fast = [&](int j, uint32_t (&P)[PW]) __attribute__((always_inline)) {
+    const float c = kI8 ? qsc * ksc_cur : a.qk_mul;
+    const float m = m_use - SoftmaxCfg<PVM>::kShift;
+    const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
+    constexpr bool kSumF16 = PVM == SAGE_PV_F16;
+    constexpr float kBound = (float)(1 << (int)(SoftmaxCfg<PVM>::kTau + SoftmaxCfg<PVM>::kShift - 1.0f));
+    float ls[2] = {0.0f, 0.0f};
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float p[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float sv = kI8 ? __int_as_float((int)S[t][v]) : (float)S[t][v];
+        p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, -bias));
+      }
+      if constexpr (!kF8) {
+#pragma unroll
+        for (int w = 0; w < 8; ++w) P[8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
+      }
+      if constexpr (!kSumF16) {
+#pragma unroll
+        for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+          for (int i = 0; i < w; ++i) p[i] += p[i + w];
+        ls[t] = p[0];
+      }
+    }
+    float part, lnew;  // the lane's sum; lsum plus it, as softmax() adds it
+    if constexpr (kSumF16) {
+      h2 hs[8];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) hs[w] = __builtin_bit_cast(h2, P[w]) + __builtin_bit_cast(h2, P[8 + w]);
+#pragma unroll
+      for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+        for (int i = 0; i < w; ++i) hs[i] = hs[i] + hs[i + w];
+      const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+      part = __builtin_amdgcn_fdot2(hs[0], ones, 0.0f, false);
+      lnew = __builtin_amdgcn_fdot2(hs[0], ones, lsum, false);
+    } else {
+      part = ls[0] + ls[1];
+      lnew = lsum + (ls[0] + ls[1]);
+    }
+    if (__builtin_amdgcn_ballot_w64(!(part <= kBound)) == 0) lsum = lnew;
+    else softmax(j, P, false);
+  };
   auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha_o;
@@ -562,7 +621,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       pend = false;
     }
     pv(sl < 0 ? (j - 1) % NBUF : (sl + NBUF - 1) % NBUF, Pprev);
-    softmax(j, Pcur, false);
+    if constexpr (PVM != SAGE_PV_FP8) softmax_fast(j, Pcur);
+    else softmax(j, Pcur, false);
     keep_p();
     qk(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF);
     sync_tiles(true);
