@@ -310,6 +310,41 @@ def test_cli_run_writes_results(tmp_path, monkeypatch, capsys):
     assert rows[0]["variant"] == "hip" and rows[0]["correctness"]["passed"] and rows[0]["effective_tops"] > 0
     assert rows[1]["variant"] == "cpu_ref" and rows[1]["cpu_threads"] >= 1
     assert (runs[0].parent / "summary.md").exists()
+    report = (runs[0].parent / "report.html").read_text()
+    assert "fake" in report and "cpu_ref" in report and "<svg" in report
+    with pytest.raises(SystemExit):
+        cli.main(["run", "--kernel", "fake", "--device", "cpu", "--timer", "cpu_wall", "--warmup-ms", "1",
+                  "--rep-ms", "5", "--output-dir", str(tmp_path / "res2"), "--no-plots"])
+    assert not list((tmp_path / "res2").glob("*/report.html"))
+
+
+def test_report_html_columns_escaping_and_no_external_resources(tmp_path):
+    from tribench_amd.harness.types import BenchResult, CorrectnessResult, EnvInfo, RunRecord
+    from tribench_amd.harness.viz import generate_run_plots, render_html
+
+    lat = dict(latency_ms_p50=1.0, latency_ms_p90=1.1, latency_ms_p95=1.2, latency_ms_p99=1.3,
+               latency_ms_min=0.9, latency_ms_max=1.4, latency_ms_mean=1.05, latency_ms_std=0.1)
+    ok = BenchResult("sage_attn", "cfg2<b>", "bf16", "contiguous", variant="hip", effective_tops=1117.4,
+                     algo_tops=1117.4, roofline_peak=5000.0, roofline_unit="int8", roofline_fraction=0.2235,
+                     prepass_ms_p50=0.12, prepass_gbps=3300.0, prepass_hbm_fraction=0.4125,
+                     correctness=CorrectnessResult(True, 5e-2, 5e-2, max_abs_err=1.2e-2, cosine=0.99995), **lat)
+    bad = BenchResult("sage_attn", "cfg3", "bf16", "contiguous", variant="hip",
+                      correctness=CorrectnessResult(False, 5e-2, 5e-2, max_abs_err=0.5), **lat)
+    cpu = BenchResult("sage_attn", "cfg2<b>", "bf16", "contiguous", variant="cpu_ref", cpu_threads=16,
+                      effective_tops=0.05, **lat)
+    rec = RunRecord(run_id="r1", env=EnvInfo(gpu_name="AMD Instinct MI355X", rocm_arch="gfx950:sramecc+:xnack-",
+                                             hip_version="7.0.1"), results=[ok, bad, cpu])
+    page = render_html(rec)
+    assert "gfx950:sramecc+:xnack-" in page and "7.0.1" in page
+    assert "cfg2&lt;b&gt;" in page and "cfg2<b>" not in page
+    assert "22.4% of 5000 int8" in page and "41.2%" in page and "0.999950" in page
+    assert page.count('<tr class="fail">') == 1 and "FAIL" in page and "cpu_ref (16 threads)" in page
+    assert "http" not in page.replace('xmlns="http://www.w3.org/2000/svg"', "") and "<script" not in page
+    # the failed row is in the table but not in the charts
+    assert page.count("cfg3") == 1
+    assert generate_run_plots(RunRecord(run_id="empty"), tmp_path) == []
+    (path,) = generate_run_plots(rec, tmp_path / "run")
+    assert path.name == "report.html" and path.read_text(encoding="utf-8") == page
 
 
 def test_cli_list_and_validate(capsys):

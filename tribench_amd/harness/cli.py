@@ -4,12 +4,13 @@
     python -m tribench_amd validate-meta
     python -m tribench_amd test --kernel sage_attn [--cases c1,c2] [--dtype bf16]
     python -m tribench_amd run  --kernel sage_attn [--cases ...] [--timer hip_event|hip_graph]
-                                [--cpu-ref] [--output-dir results]
+                                [--cpu-ref] [--no-plots] [--output-dir results]
 
 Subcommands, options and exit codes follow cli.py:11-61, 205-582 of the
 reference: every implementation of a pack (its ``triton`` entrypoint when
 present, then each variant) is checked against the pack's reference on the
-same seeded inputs; ``run`` times them and writes run.json / summary.md.
+same seeded inputs; ``run`` times them and writes run.json, summary.md and
+report.html (``viz.py``; ``--no-plots`` leaves it out).
 ``run`` adds effective TOPS, the roofline fraction and, with ``--cpu-ref``, a
 ``cpu_ref`` row timing the pack's reference on this host's cores.
 """
@@ -48,6 +49,7 @@ def _build_parser() -> argparse.ArgumentParser:
     r.add_argument("--output-dir", default="results")
     r.add_argument("--no-correctness", action="store_true")
     r.add_argument("--cpu-ref", action="store_true", help="also time the reference on the host CPU")
+    r.add_argument("--no-plots", action="store_true", help="do not write report.html")
     return p
 
 
@@ -257,6 +259,10 @@ def _cmd_run(args) -> int:
     json_path = write_json(record, args.output_dir)
     md_path = write_summary_md(record, args.output_dir)
     print(f"\nResults saved to: {json_path.parent}\n   JSON:     {json_path}\n   Summary:  {md_path}")
+    if not args.no_plots:
+        from .viz import generate_run_plots
+        for p in generate_run_plots(record, json_path.parent):
+            print(f"   Report:   {p}")
     return 1 if failed else 0
 
 
