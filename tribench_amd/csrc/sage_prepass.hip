@@ -92,11 +92,18 @@ constexpr int vtile_pool_bytes() {
 // the block max and not stored.  NI = 16-element items per thread
 // (blk * D / 4096, at least 1; with fewer items than threads whole waves idle).
 // ---------------------------------------------------------------------------
-template <typename T, int D, int NI>
+struct NoHook {
+  __device__ void operator()() const {}
+};
+
+// after_loads() runs once the block's loads are issued and before km_s is
+// read: a caller that fills km_s there (with a barrier) overlaps that work
+// with the loads in flight.
+template <typename T, int D, int NI, typename AfterLoads = NoHook>
 __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
                             int q_sub, bool use_mul, float mul, const float* km_s,
                             int8_t* __restrict__ dst, int64_t dn, float* __restrict__ scale_dst,
-                            uint32_t* amax_s, float* scl_s, float* rcp_s) {
+                            uint32_t* amax_s, float* scl_s, float* rcp_s, AfterLoads after_loads = {}) {
   constexpr int CPR = D / 16;  // 16-element items per row
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -104,12 +111,6 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
   const int nsub = blk / q_sub;
 
   if (tid < 16) amax_s[tid] = 0u;
-  // the thread's 16 channels are the same in every item (256 % CPR == 0):
-  // their means go to registers once, not through LDS for every element
-  static_assert(kPrepassThreads % CPR == 0, "items of a thread share their channels");
-  float kmr[16];
-#pragma unroll
-  for (int e = 0; e < 16; ++e) kmr[e] = km_s ? km_s[(tid % CPR) * 16 + e] : 0.0f;
   Raw8<T> raw[NI][2];
   float amx[NI];
 #pragma unroll
@@ -125,6 +126,13 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
       raw[j][1] = zero8<T>();
     }
   }
+  after_loads();
+  // the thread's 16 channels are the same in every item (256 % CPR == 0):
+  // their means go to registers once, not through LDS for every element
+  static_assert(kPrepassThreads % CPR == 0, "items of a thread share their channels");
+  float kmr[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) kmr[e] = km_s ? km_s[(tid % CPR) * 16 + e] : 0.0f;
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int it = tid + kPrepassThreads * j;
@@ -355,9 +363,9 @@ __device__ __forceinline__ void quant_q_role(const PrepassArgs& a, int64_t r, ui
                         sdst, amax_s, scl_s, rcp_s);
 }
 
-template <typename T, int D, int NI>
+template <typename T, int D, int NI, typename AfterLoads = NoHook>
 __device__ __forceinline__ void quant_k_role(const PrepassArgs& a, int64_t r, const float* km_s, uint32_t* amax_s,
-                             float* scl_s, float* rcp_s) {
+                             float* scl_s, float* rcp_s, AfterLoads after_loads = {}) {
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
   const int64_t row0 = kb * a.blkk;
   const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
@@ -365,7 +373,7 @@ __device__ __forceinline__ void quant_k_role(const PrepassArgs& a, int64_t r, co
   int8_t* dst = a.k8 + b * a.sk8[0] + h * a.sk8[1] + row0 * a.sk8[2];
   float* sdst = a.k_scale + (b * a.Hkv + h) * a.nkb + kb;
   quant_block<T, D, NI>(src, a.sk[2], rows_valid, a.blkk, a.blkk, false, 1.0f, km_s, dst, a.sk8[2], sdst,
-                        amax_s, scl_s, rcp_s);
+                        amax_s, scl_s, rcp_s, after_loads);
 }
 
 // NIQ / NIK: 16-element items per thread of a Q / K block (blk * D / 4096).
@@ -403,9 +411,9 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_a_kernel(PrepassArgs 
   if (r < a.n_vt_a) vtile_role<T, D>(a, r, nullptr, pool);  // fp16 / bf16 tiles
 }
 
-// Channel mean of K (km_s) and FP8 V scale (vs_s) of one (batch, head) from
-// launch A's per-chunk partials, into LDS (threads < D); the K block 0 role
-// also writes them out.
+// Channel mean of K (km_s) and FP8 V scale (vs_s, unless null) of one
+// (batch, head) from launch A's per-chunk partials, into LDS (threads < D);
+// the K block 0 role also writes them out.
 template <int D>
 __device__ __forceinline__ void head_stats(const PrepassArgs& a, int64_t b, int64_t h, bool write_out,
                                            float* km_s, float* vs_s) {
@@ -425,7 +433,7 @@ __device__ __forceinline__ void head_stats(const PrepassArgs& a, int64_t b, int6
     km_s[tid] = m;
     if (write_out) a.km[(b * a.Hkv + h) * D + tid] = m;
   }
-  if (a.v_fp8) {
+  if (a.v_fp8 && vs_s) {
     float m = a.pamax[base + tid];
 #pragma unroll
     for (int c = 1; c < 16; ++c)
@@ -457,9 +465,12 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs 
     return;
   }
   const int64_t kb = r % a.nkb, h = (r / a.nkb) % a.Hkv, b = r / (a.nkb * a.Hkv);
-  head_stats<D>(a, b, h, kb == 0, km_s, vs_s);
-  __syncthreads();
-  quant_k_role<T, D, NIK>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s);
+  // the head's channel means (and the V scales that this block's FP8 V rows
+  // or output need) are formed while the K block's loads are in flight
+  quant_k_role<T, D, NIK>(a, r, a.smooth_k ? km_s : nullptr, amax_s, scl_s, rcp_s, [&]() {
+    head_stats<D>(a, b, h, kb == 0, km_s, a.v_rows || kb == 0 ? vs_s : nullptr);
+    __syncthreads();
+  });
   if (a.v_rows) {
     const int64_t row0 = kb * a.blkk;
     const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
