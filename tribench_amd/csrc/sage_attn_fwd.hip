@@ -374,9 +374,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 
   // ---- building blocks
   // S^T of block j (its K tile in slot j % NBUF): K row 32t + n, bytes 32c + 16hh
-  auto qk = [&](int j, int sl) __attribute__((always_inline)) {  // sl = j % NBUF
+  // (into the S buffer Sd, its k scale into kd)
+  auto qk_into = [&](int j, int sl, SAcc (&Sd)[2], float& kd) __attribute__((always_inline)) {  // sl = j % NBUF
     const char* ks = smem + sl * SLOT;
-    if constexpr (kI8) ksc_cur = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
+    if constexpr (kI8) kd = ksc_base[min(j >> a.blkk_shift, a.nks - 1)];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       v4i ka[KC];
@@ -385,18 +386,19 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int c = 0; c < KC; ++c) {
         if constexpr (kI8) {
-          S[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qreg[c], c == 0 ? magic : S[t], 0, 0, 0);
+          Sd[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka[c], qreg[c], c == 0 ? magic : Sd[t], 0, 0, 0);
         } else if constexpr (QKM == kQkF16) {
-          S[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ka[c]), __builtin_bit_cast(v8h, qreg[c]),
-                                                        c == 0 ? (v16f){} : S[t], 0, 0, 0);
+          Sd[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ka[c]), __builtin_bit_cast(v8h, qreg[c]),
+                                                         c == 0 ? (v16f){} : Sd[t], 0, 0, 0);
         } else {
-          S[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ka[c]),
-                                                         __builtin_bit_cast(v8bf, qreg[c]), c == 0 ? (v16f){} : S[t],
-                                                         0, 0, 0);
+          Sd[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, ka[c]),
+                                                          __builtin_bit_cast(v8bf, qreg[c]), c == 0 ? (v16f){} : Sd[t],
+                                                          0, 0, 0);
         }
       }
     }
   };
+  auto qk = [&](int j, int sl) __attribute__((always_inline)) { qk_into(j, sl, S, ksc_cur); };
   // O^T += V^T P^T of block j (its V^T tile in slot j % NBUF)
   auto pv = [&](int sl, const uint32_t (&P)[PW]) __attribute__((always_inline)) {  // sl = j % NBUF
     const char* vs = smem + sl * SLOT;
@@ -429,10 +431,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // softmax of block j held in S -> P (and the running max / sums).  Max and
   // sum are pairwise trees, not serial chains, to keep dependency depth low.
   // c > 0 scales S to log2 units: q_scale * k_scale (INT8) or qk_mul.
-  auto softmax = [&](int j, uint32_t (&P)[PW], bool masked) __attribute__((always_inline)) {
+  // (softmax_on: of the S buffer Sx with k scale kx)
+  auto softmax_on = [&](int j, uint32_t (&P)[PW], bool masked, const SAcc (&Sx)[2], float kx)
+                        __attribute__((always_inline)) {
     const int k0 = j * kBN;
     const int qrow = qa + n;
-    const float c = kI8 ? qsc * ksc_cur : a.qk_mul;
+    const float c = kI8 ? qsc * kx : a.qk_mul;
     float mblk;
     if constexpr (kI8) {
       int x[32];
@@ -440,7 +444,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          x[16 * t + v] = S[t][v];
+          x[16 * t + v] = Sx[t][v];
           if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = INT_MIN;
         }
 #pragma unroll
@@ -455,7 +459,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          x[16 * t + v] = S[t][v];
+          x[16 * t + v] = Sx[t][v];
           if (masked && !key_ok(k0 + key_of(t, v), qrow)) x[16 * t + v] = -INFINITY;
         }
 #pragma unroll
@@ -486,7 +490,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       float p[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float sv = kI8 ? __int_as_float((int)S[t][v]) : (float)S[t][v];
+        const float sv = kI8 ? __int_as_float((int)Sx[t][v]) : (float)Sx[t][v];
         float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, -bias));
         if (masked) e = key_ok(k0 + key_of(t, v), qrow) ? e : 0.0f;
         p[v] = e;
@@ -519,6 +523,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lsum += ls[0] + ls[1];
     }
   };
+  auto softmax = [&](int j, uint32_t (&P)[PW], bool masked) __attribute__((always_inline)) {
+    softmax_on(j, P, masked, S, ksc_cur);
+  };
   // Mask-free block, row max not recomputed: P is formed against the running
   // max m_use straight away.  softmax() keeps m_use too unless the block max
   // exceeds it by more than kTau, that is unless some P exceeds
@@ -532,8 +539,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // scores fail the test.  Otherwise softmax() redoes the block from the
   // untouched S.  Not used for FP8 P: with kShift = 6 the sums of a typical
   // block exceed the bound.
-  auto softmax_fast = [&](int j, uint32_t (&P)[PW]) __attribute__((always_inline)) {
-    const float c = kI8 ? qsc * ksc_cur : a.qk_mul;
+  auto softmax_fast_on = [&](int j, uint32_t (&P)[PW], const SAcc (&Sx)[2], float kx) __attribute__((always_inline)) {
+    const float c = kI8 ? qsc * kx : a.qk_mul;
     const float m = m_use - SoftmaxCfg<PVM>::kShift;
     const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
     constexpr bool kSumF16 = PVM == SAGE_PV_F16;
@@ -544,7 +551,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       float p[16];
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float sv = kI8 ? __int_as_float((int)S[t][v]) : (float)S[t][v];
+        const float sv = kI8 ? __int_as_float((int)Sx[t][v]) : (float)Sx[t][v];
         p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sv, c, -bias));
       }
       if constexpr (!kF8) {
@@ -576,7 +583,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       lnew = lsum + (ls[0] + ls[1]);
     }
     if (__builtin_amdgcn_ballot_w64(!(part <= kBound)) == 0) lsum = lnew;
-    else softmax(j, P, false);
+    else softmax_on(j, P, false, Sx, kx);
+  };
+  auto softmax_fast = [&](int j, uint32_t (&P)[PW]) __attribute__((always_inline)) {
+    softmax_fast_on(j, P, S, ksc_cur);
   };
   auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -625,6 +635,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else softmax(j, Pcur, false);
     keep_p();
     qk(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF);
+    sync_tiles(true);
+  };
+
+  // INT8 at D = 128 with fp16 P: the S of block j+1 goes to a second buffer,
+  // so that its QK MFMAs share one basic block with the P.V MFMAs of block j-1
+  // and the softmax of block j (the scheduler interleaves all three; measured
+  // -1.9 % per launch at config 2, while with FP8 P it was slower).  Two
+  // iterations per trip swap the buffers' roles.
+  constexpr bool kTwoS = kI8 && D == 128 && PVM == SAGE_PV_F16;
+  SAcc S2[2];
+  float ksc2 = 0.0f;
+  auto fused_iter = [&](int j, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb) __attribute__((always_inline)) {
+    load_tile(j + 3, (j + 3) % NBUF);
+    if (pend) {
+      rescale_o();
+      pend = false;
+    }
+    pv((j - 1) % NBUF, Pprev);
+    qk_into(j + 1, (j + 1) % NBUF, Sb, kb);
+    softmax_fast_on(j, Pcur, Sa, ka);
+    keep_p();
     sync_tiles(true);
   };
 
@@ -719,6 +750,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       fast_iter(j + 2, 3);
       fast_iter(j + 3, 4);
       fast_iter(j + 4, 0);
+    }
+  if constexpr (kTwoS)
+    for (; j + 2 <= j_fast; j += 2) {
+      fused_iter(j, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 1, S2, ksc2, S, ksc_cur);
     }
   for (; j < j_fast; ++j) fast_iter(j, -1);
   for (; j <= nkb; ++j) generic_iter(j);
