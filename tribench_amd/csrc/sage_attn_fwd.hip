@@ -638,22 +638,24 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sync_tiles(true);
   };
 
-  // INT8 at D = 128 with fp16 P: the S of block j+1 goes to a second buffer,
-  // so that its QK MFMAs share one basic block with the P.V MFMAs of block j-1
-  // and the softmax of block j (the scheduler interleaves all three; measured
-  // -1.9 % per launch at config 2, while with FP8 P it was slower).  Two
-  // iterations per trip swap the buffers' roles.
-  constexpr bool kTwoS = kI8 && D == 128 && PVM == SAGE_PV_F16;
+  // INT8 with fp16 P: the S of block j+1 goes to a second buffer, so that its
+  // QK MFMAs share one basic block with the P.V MFMAs of block j-1 and the
+  // softmax of block j (the scheduler interleaves all three; measured -1.9 %
+  // per launch at config 2 and -1.2 % at config 4, while with FP8 P it was
+  // slower).  Two iterations per trip swap the buffers' roles (ten at D = 64,
+  // where the ring slots are constants too).  sl as for fast_iter.
+  constexpr bool kTwoS = kI8 && PVM == SAGE_PV_F16;
   SAcc S2[2];
   float ksc2 = 0.0f;
-  auto fused_iter = [&](int j, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb) __attribute__((always_inline)) {
-    load_tile(j + 3, (j + 3) % NBUF);
+  auto fused_iter = [&](int j, int sl, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb)
+                        __attribute__((always_inline)) {
+    load_tile(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
     if (pend) {
       rescale_o();
       pend = false;
     }
-    pv((j - 1) % NBUF, Pprev);
-    qk_into(j + 1, (j + 1) % NBUF, Sb, kb);
+    pv(sl < 0 ? (j - 1) % NBUF : (sl + NBUF - 1) % NBUF, Pprev);
+    qk_into(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF, Sb, kb);
     softmax_fast_on(j, Pcur, Sa, ka);
     keep_p();
     sync_tiles(true);
@@ -740,9 +742,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int j_fast = min(min(nfull, jmax), nkb - 3);
   generic_iter(0);
   int j = 1;
-  // INT8 at D = 64 with fp16 P: five iterations per trip with constant ring
-  // slots (elsewhere the copies run out of registers); j % NBUF == 1 at every
-  // trip
+  // INT8 at D = 64 with fp16 P: constant ring slots, j % NBUF == 1 at every
+  // trip (at D = 128 the copies run out of registers)
+  if constexpr (kTwoS && D == 64)
+    for (; j + 2 * NBUF <= j_fast; j += 2 * NBUF) {
+      fused_iter(j, 1, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 1, 2, S2, ksc2, S, ksc_cur);
+      fused_iter(j + 2, 3, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 3, 4, S2, ksc2, S, ksc_cur);
+      fused_iter(j + 4, 0, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 5, 1, S2, ksc2, S, ksc_cur);
+      fused_iter(j + 6, 2, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 7, 3, S2, ksc2, S, ksc_cur);
+      fused_iter(j + 8, 4, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 9, 0, S2, ksc2, S, ksc_cur);
+    }
   if constexpr (kI8 && D == 64 && PVM == SAGE_PV_F16)
     for (; j + NBUF <= j_fast; j += NBUF) {
       fast_iter(j, 1);
@@ -751,10 +765,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       fast_iter(j + 3, 4);
       fast_iter(j + 4, 0);
     }
-  if constexpr (kTwoS)
+  if constexpr (kTwoS && D == 128)
     for (; j + 2 <= j_fast; j += 2) {
-      fused_iter(j, S, ksc_cur, S2, ksc2);
-      fused_iter(j + 1, S2, ksc2, S, ksc_cur);
+      fused_iter(j, -1, S, ksc_cur, S2, ksc2);
+      fused_iter(j + 1, -1, S2, ksc2, S, ksc_cur);
     }
   for (; j < j_fast; ++j) fast_iter(j, -1);
   for (; j <= nkb; ++j) generic_iter(j);
