@@ -638,13 +638,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     sync_tiles(true);
   };
 
-  // INT8 with fp16 P: the S of block j+1 goes to a second buffer, so that its
-  // QK MFMAs share one basic block with the P.V MFMAs of block j-1 and the
-  // softmax of block j (the scheduler interleaves all three; measured -1.9 %
-  // per launch at config 2 and -1.2 % at config 4, while with FP8 P it was
-  // slower).  Two iterations per trip swap the buffers' roles (ten at D = 64,
-  // where the ring slots are constants too).  sl as for fast_iter.
-  constexpr bool kTwoS = kI8 && PVM == SAGE_PV_F16;
+  // INT8 with fp16 P, and fp16/bf16 QK at D = 64: the S of block j+1 goes to
+  // a second buffer, so that its QK MFMAs share one basic block with the P.V
+  // MFMAs of block j-1 and the softmax of block j (the scheduler interleaves
+  // all three; measured -1.9 % per launch at config 2, -1.2 % at config 4,
+  // -3 to -4.5 % for fp16/bf16 QK at D = 64; with FP8 P it was slower, and
+  // fp16/bf16 QK at D = 128 has no registers left for it).  Two iterations
+  // per trip swap the buffers' roles (ten at D = 64, where the ring slots are
+  // constants too).  sl as for fast_iter.
+  constexpr bool kTwoS = (kI8 && PVM == SAGE_PV_F16) || (!kI8 && D == 64);
   SAcc S2[2];
   float ksc2 = 0.0f;
   auto fused_iter = [&](int j, int sl, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb)
