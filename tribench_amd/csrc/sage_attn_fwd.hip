@@ -647,6 +647,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // per trip swap the buffers' roles (ten at D = 64, where the ring slots are
   // constants too).  sl as for fast_iter.
   constexpr bool kTwoS = (kI8 && PVM == SAGE_PV_F16) || (!kI8 && D == 64);
+  static_assert(!(kTwoS && PVM == SAGE_PV_FP8), "fused_iter uses the fp16/bf16 P shortcut of softmax_fast_on");
   SAcc S2[2];
   float ksc2 = 0.0f;
   auto fused_iter = [&](int j, int sl, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb)
@@ -744,8 +745,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int j_fast = min(min(nfull, jmax), nkb - 3);
   generic_iter(0);
   int j = 1;
-  // INT8 at D = 64 with fp16 P: constant ring slots, j % NBUF == 1 at every
-  // trip (at D = 128 the copies run out of registers)
+  // D = 64 (INT8 with fp16 P, and fp16/bf16 QK): constant ring slots, j % NBUF
+  // == 1 at every trip (at D = 128 the copies run out of registers); then
+  // INT8 with fp16 P five at a time with one S buffer
   if constexpr (kTwoS && D == 64)
     for (; j + 2 * NBUF <= j_fast; j += 2 * NBUF) {
       fused_iter(j, 1, S, ksc_cur, S2, ksc2);
