@@ -60,6 +60,14 @@ SMALL = [
     (2, 4, 2, 300, 128, "bf16", True, "fp16", "thread", 2.0),  # per-row Q scales
     (1, 3, 3, 1000, 64, "fp16", False, "fp16", "thread", 4.0),
     (1, 2, 2, 777, 128, "bf16", True, "fp16", "thread", 2.0),
+    # non-causal N = 64 * nkb runs nkb - 4 mask-free iterations (blocks 1 ..
+    # nkb - 4), in trips of 2 at D = 128 and of 10, then 5, at D = 64, then
+    # one at a time: these end the trips with and without leftovers
+    (1, 2, 2, 448, 128, "bf16", False, "fp16", "block", 2.0),   # 3 = one 2-trip + 1
+    (1, 2, 2, 512, 128, "bf16", False, "fp16", "wave", 2.0),    # 4 = two 2-trips
+    (1, 2, 1, 896, 64, "bf16", False, "fp16", "block", 2.0),    # 10 = one 10-trip
+    (1, 2, 2, 1216, 64, "fp16", False, "fp16", "block", 2.0),   # 15 = 10 + 5
+    (1, 1, 1, 1408, 64, "bf16", False, "fp16", "thread", 2.0),  # 18 = 10 + 5 + 3
 ]
 
 

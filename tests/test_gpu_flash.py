@@ -88,6 +88,10 @@ SMALL = [
     (1, 3, 3, 1000, 1000, 128, "fp16", False),
     (1, 2, 1, 130, 700, 128, "bf16", False),
     (1, 2, 2, 1, 500, 64, "fp16", False),
+    # D = 64: 10 and 18 mask-free iterations (one 10-block trip; one trip and
+    # 8 single iterations)
+    (1, 2, 2, 896, 896, 64, "fp16", False),
+    (1, 2, 1, 1408, 1408, 64, "bf16", False),
 ]
 
 
