@@ -244,42 +244,44 @@ def _expand_kv(x, hq):
 
 
 def sdpa(q, k, v, causal: bool = False, sm_scale: float | None = None, dtype=np.float64,
-         q_chunk: int = 1024):
+         q_chunk: int = 1024, rows=None):
     """softmax(q k^T * sm_scale [+ causal mask]) v (reference.py:15-24).
 
     The causal mask is the reference's torch.tril(ones(N, N)) == 0 (key j is
     masked for query i iff j > i).  KV heads are repeated for GQA
     (repeat_interleave over the head dim).  Computed in ``dtype`` per
     (batch, head, chunk of q rows) so the score matrix is never whole.
+    ``rows`` (query indices) restricts the result to those rows, in that
+    order: [B, Hq, len(rows), D].
     """
     q = np.asarray(q)
     B, Hq, Nq, D = q.shape
     Nkv = k.shape[2]
     if sm_scale is None:
         sm_scale = D ** -0.5
-    out = np.empty((B, Hq, Nq, D), dtype=dtype)
+    rows = np.arange(Nq) if rows is None else np.asarray(rows, dtype=np.int64)
+    out = np.empty((B, Hq, len(rows), D), dtype=dtype)
     G = Hq // k.shape[1]
+    kj = np.arange(Nkv)[None, :]
     for b in range(B):
         for h in range(Hq):
             kk = np.asarray(k[b, h // G], dtype=dtype)
             vv = np.asarray(v[b, h // G], dtype=dtype)
-            for i0 in range(0, Nq, q_chunk):
-                i1 = min(i0 + q_chunk, Nq)
-                s = np.asarray(q[b, h, i0:i1], dtype=dtype) @ kk.T
+            for i0 in range(0, len(rows), q_chunk):
+                r = rows[i0:i0 + q_chunk]
+                s = np.asarray(q[b, h, r], dtype=dtype) @ kk.T
                 s *= dtype(sm_scale)
                 if causal:
-                    qi = np.arange(i0, i1)[:, None]
-                    kj = np.arange(Nkv)[None, :]
-                    s = np.where(kj > qi, -np.inf, s)
+                    s = np.where(kj > r[:, None], -np.inf, s)
                 s -= s.max(axis=1, keepdims=True)
                 np.exp(s, out=s)
                 s /= s.sum(axis=1, keepdims=True)
-                out[b, h, i0:i1] = s @ vv
+                out[b, h, i0:i0 + len(r)] = s @ vv
     return out
 
 
 def sage_emulate(q8, q_scale, k8, k_scale, v, causal=False, blkq=128, q_sub=None, blkk=64,
-                 v_scale=None, q_chunk: int = 1024):
+                 v_scale=None, q_chunk: int = 1024, rows=None):
     """The SageAttention algorithm of triton_impl.py:86-160 in exact arithmetic.
 
     Scores are int8 dot products times q_scale * k_scale (log2 units: the
@@ -287,33 +289,35 @@ def sage_emulate(q8, q_scale, k8, k_scale, v, causal=False, blkq=128, q_sub=None
     fp64.  ``v`` is either real values or FP8 codes with ``v_scale``.  The
     difference between this and :func:`sdpa` is the quantization error; the
     difference between this and the kernel is the kernel's own arithmetic.
+    ``rows`` (query indices) restricts the result to those rows, in that
+    order: [B, Hq, len(rows), D].
     """
     q_sub = blkq if q_sub is None else q_sub
     B, Hq, Nq, D = q8.shape
     Hkv, Nkv = k8.shape[1], k8.shape[2]
     G = Hq // Hkv
-    if v_scale is not None:
-        vv_all = e4m3_decode(v).astype(np.float64) * np.asarray(v_scale, np.float64)[:, :, None, :]
-    else:
-        vv_all = np.asarray(v, dtype=np.float64)
-    out = np.empty((B, Hq, Nq, D), dtype=np.float64)
+    rows_all = np.arange(Nq) if rows is None else np.asarray(rows, dtype=np.int64)
+    out = np.empty((B, Hq, len(rows_all), D), dtype=np.float64)
     kcol = np.arange(Nkv)
     for b in range(B):
-        for h in range(Hq):
-            hk = h // G
+        for hk in range(Hkv):
+            if v_scale is not None:
+                vv = e4m3_decode(v[b, hk]).astype(np.float64) * np.asarray(v_scale[b, hk], np.float64)[None, :]
+            else:
+                vv = np.asarray(v[b, hk], dtype=np.float64)
             kk = k8[b, hk].astype(np.float64)
             ks = np.asarray(k_scale[b, hk], np.float64)[kcol // blkk]
-            for i0 in range(0, Nq, q_chunk):
-                i1 = min(i0 + q_chunk, Nq)
-                rows = np.arange(i0, i1)
-                qs = np.asarray(q_scale[b, h], np.float64)[rows // q_sub]
-                s = (q8[b, h, i0:i1].astype(np.float64) @ kk.T) * qs[:, None] * ks[None, :]
-                if causal:
-                    s = np.where(kcol[None, :] > rows[:, None], -np.inf, s)
-                s -= s.max(axis=1, keepdims=True)
-                p = np.exp2(s)
-                p /= p.sum(axis=1, keepdims=True)
-                out[b, h, i0:i1] = p @ vv_all[b, hk]
+            for h in range(hk * G, (hk + 1) * G):
+                for i0 in range(0, len(rows_all), q_chunk):
+                    r = rows_all[i0:i0 + q_chunk]
+                    qs = np.asarray(q_scale[b, h], np.float64)[r // q_sub]
+                    s = (q8[b, h, r].astype(np.float64) @ kk.T) * qs[:, None] * ks[None, :]
+                    if causal:
+                        s = np.where(kcol[None, :] > r[:, None], -np.inf, s)
+                    s -= s.max(axis=1, keepdims=True)
+                    p = np.exp2(s)
+                    p /= p.sum(axis=1, keepdims=True)
+                    out[b, h, i0:i0 + len(r)] = p @ vv
     return out
 
 

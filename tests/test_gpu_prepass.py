@@ -232,3 +232,18 @@ def test_prepass_vt_equals_separate_calls(case, pack_ref, hip_impl, gpu_device):
     assert torch.equal(fused["vt"], tiles)
     for key in ("q8", "q_scale", "k8", "k_scale") + (("km",) if smooth else ()) + (("v_scale",) if pv == "fp8" else ()):
         assert torch.equal(fused[key], plain[key]), key
+
+
+def test_vtiles_of_another_pv_type_are_rejected(pack_ref, hip_impl, gpu_device):
+    """fp16 and bf16 V tiles have the same size: a pre-pass result made for one
+    P.V type must not be read as the other (an "invalid argument" error)."""
+    inp = _inputs(pack_ref, 1, 2, 2, 128, 64, "bf16", 2.0, "normal")
+    q, k, v = (inp[x].to(gpu_device) for x in ("q", "k", "v"))
+    pre = hip_impl.prepass(q, k, v, pv_dtype="fp16")
+    assert pre["vt_pv"] == "fp16"
+    with pytest.raises(ValueError, match="invalid argument"):
+        hip_impl.attention(q, k, v, pre, pv_dtype="bf16")
+    with pytest.raises(ValueError, match="invalid argument"):
+        hip_impl.attention_q(q, k, v, pre, pv_dtype="bf16")
+    hip_impl.attention(q, k, v, pre, pv_dtype="fp16")  # the matching type is accepted
+    torch.cuda.synchronize()

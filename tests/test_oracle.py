@@ -288,6 +288,29 @@ def test_emulation_is_base2_sdpa_of_dequantized_inputs():
             assert np.abs(emu - ref).max() < 1e-12
 
 
+def test_row_subsets_equal_the_full_result():
+    """``rows=`` (the sampled-row checks at full size) picks the same rows as
+    the full computation, in the given order, causal and GQA included, with
+    the FP8-code form of V too (to rounding: BLAS may sum a product of
+    another shape in another order; a wrong row is off by O(1))."""
+    rng = np.random.default_rng(11)
+    B, Hq, Hkv, N, D = 2, 4, 2, 150, 32
+    q = rng.standard_normal((B, Hq, N, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hkv, N, D)).astype(np.float32)
+    rows = np.array([149, 0, 3, 64, 127, 128, 77])
+    q8, qs = O.quant_per_block_int8(q, 128, mul=O.q_multiplier(D), q_sub=32)
+    k8, ks = O.quant_per_block_int8(k, 64)
+    codes, vs = O.quant_v_fp8(v)
+    for causal in (False, True):
+        full = O.sdpa(q, k, v, causal=causal, q_chunk=16)
+        assert np.abs(O.sdpa(q, k, v, causal=causal, q_chunk=16, rows=rows) - full[:, :, rows]).max() < 1e-12
+        for vv, vsc in ((v, None), (codes, vs)):
+            e = O.sage_emulate(q8, qs, k8, ks, vv, causal=causal, q_sub=32, v_scale=vsc, q_chunk=16)
+            er = O.sage_emulate(q8, qs, k8, ks, vv, causal=causal, q_sub=32, v_scale=vsc, q_chunk=4, rows=rows)
+            assert np.abs(er - e[:, :, rows]).max() < 1e-12
+
+
 # ---------------------------------------------------------------------------
 # fixtures and work formulas
 # ---------------------------------------------------------------------------

@@ -336,6 +336,46 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       __builtin_amdgcn_global_load_lds((gmem_t*)src, (lmem_t*)dst, 16, 0, 0);
     }
   };
+  // Tile loads of the mask-free loop: only whole K tiles (every row < Nkv),
+  // so each of the wave's LPW loads is a uniform tile base plus a lane offset
+  // that does not change from tile to tile.
+  uint32_t foff[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int g = wave + NW * i;
+    if (g < KLD) {
+      const int p = 64 * g + lane;
+      const int r = p / (KRB / 16), pc = p % (KRB / 16);
+      foff[i] = (uint32_t)(r * a.skn * QEB + 16 * (pc ^ swz<KRB>(r)));
+    } else if (g < KLD + VLD) {
+      const int p = 64 * (g - KLD) + lane;
+      const int d = p / (VRB / 16), pc = p % (VRB / 16);
+      foff[i] = (uint32_t)(d * VRB + 16 * (pc ^ swz<VRB>(d)));
+    } else {
+      foff[i] = 0;
+    }
+  }
+  const int64_t ktile_bytes = (int64_t)kBN * a.skn * QEB;
+  auto load_tile_fast = [&](int j, int sl) __attribute__((always_inline)) {  // sl = j % NBUF
+    char* slot = smem + sl * SLOT;
+#pragma unroll
+    for (int i = 0; i < LPW; ++i) {
+      const int g = wave + NW * i;  // wave-uniform
+      const char* base;
+      char* dst;
+      if (g < KLD) {
+        base = kbase + j * ktile_bytes;
+        dst = slot + 1024 * g;
+      } else if (g < KLD + VLD) {
+        base = reinterpret_cast<const char*>(vtbase) + (int64_t)j * VTB;
+        dst = slot + KTB + 1024 * (g - KLD);
+      } else {
+        base = kbase;
+        dst = smem + NBUF * SLOT;
+      }
+      __builtin_amdgcn_global_load_lds((gmem_t*)(base + foff[i]), (lmem_t*)dst, 16, 0, 0);
+    }
+  };
   // end of an iteration: this wave's loads of the tile needed next are done
   // (at most `ahead` younger tiles in flight), its LDS reads are done, barrier
   auto sync_tiles = [&](bool ahead) __attribute__((always_inline)) {
@@ -625,7 +665,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // sl: j % NBUF as a constant (the unrolled loop: operand offsets fold into
   // the LDS instructions), or -1 to compute the slots from j
   auto fast_iter = [&](int j, int sl) __attribute__((always_inline)) {
-    load_tile(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
+    load_tile_fast(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
     if (pend) {
       rescale_o();
       pend = false;
@@ -652,7 +692,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   float ksc2 = 0.0f;
   auto fused_iter = [&](int j, int sl, SAcc (&Sa)[2], float ka, SAcc (&Sb)[2], float& kb)
                         __attribute__((always_inline)) {
-    load_tile(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
+    load_tile_fast(j + 3, sl < 0 ? (j + 3) % NBUF : (sl + 3) % NBUF);
     if (pend) {
       rescale_o();
       pend = false;
@@ -742,7 +782,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   sync_tiles(nkb > 2);
   if (jmax >= 0) qk(0, 0);
 
-  const int j_fast = min(min(nfull, jmax), nkb - 3);
+  const int j_fast = min(min(nfull, jmax), min(nkb, a.Nkv / kBN) - 3);  // tile j+3 whole
   generic_iter(0);
   int j = 1;
   // D = 64 (INT8 with fp16 P, and fp16/bf16 QK): constant ring slots, j % NBUF

@@ -254,6 +254,7 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         out["v_scale"] = v_scale
     if vt is not None:
         out["vt"] = vt
+        out["vt_pv"] = pv_dtype  # the tiles' element type: attention() checks it against its pv_dtype
     return out
 
 
@@ -295,6 +296,21 @@ def per_block_int8(q, k, km=None, BLKQ=128, BLKK=64, sm_scale=None, tensor_layou
     return r["q8"], r["q_scale"], r["k8"], r["k_scale"]
 
 
+def _tiles_for(pre, v, pv_dtype, B, Hkv, Nkv, D, tensor_layout):
+    """The V tiles the attention kernel reads: ``pre["vt"]`` when present (it
+    must hold ``pv_dtype`` elements: fp16 and bf16 tiles have the same size,
+    so a mismatch would otherwise be read as the wrong type), else built from v."""
+    vt = pre.get("vt")
+    if vt is None:
+        return vtiles(v, pv_dtype, pre.get("v_scale"), tensor_layout=tensor_layout)
+    if pre.get("vt_pv") != pv_dtype:
+        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] holds {pre.get('vt_pv')!r} tiles, "
+                         f"the attention was asked for pv_dtype {pv_dtype!r}")
+    if vt.numel() < _load().sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype]):
+        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] is not a {pv_dtype} tile buffer")
+    return vt
+
+
 def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=128, blkk=64, tensor_layout="HND",
               out=None):
     """Launch the fused attention kernel on the outputs of :func:`prepass`.
@@ -308,11 +324,7 @@ def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=12
         raise ValueError(f"sage_attn hip: invalid argument: pv_dtype {pv_dtype!r}")
     B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v, tensor_layout)
     o = _empty_like_layout(q, q.dtype) if out is None else out
-    vt = pre.get("vt")
-    if vt is None:
-        vt = vtiles(v, pv_dtype, pre.get("v_scale"), tensor_layout=tensor_layout)
-    elif vt.numel() < lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype]):
-        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] is not a {pv_dtype} tile buffer")
+    vt = _tiles_for(pre, v, pv_dtype, B, Hkv, Nkv, D, tensor_layout)
     rc = lib.sage_attn_fwd(
         _ptr(pre["q8"]), _strides(pre["q8"], tensor_layout), _ptr(pre["q_scale"]),
         _ptr(pre["k8"]), _strides(pre["k8"], tensor_layout), _ptr(pre["k_scale"]),
@@ -339,11 +351,7 @@ def attention_q(q, k, v, pre, causal=False, sm_scale=None, *, pv_dtype="fp16", q
         sm_scale = D ** -0.5
     q_mul = float(np.float32(sm_scale * LOG2E_REF))
     o = _empty_like_layout(q, q.dtype) if out is None else out
-    vt = pre.get("vt")
-    if vt is None:
-        vt = vtiles(v, pv_dtype, pre.get("v_scale"), tensor_layout=tensor_layout)
-    elif vt.numel() < lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype]):
-        raise ValueError(f"sage_attn hip: invalid argument: pre['vt'] is not a {pv_dtype} tile buffer")
+    vt = _tiles_for(pre, v, pv_dtype, B, Hkv, Nkv, D, tensor_layout)
     if q8_out is not None and (q8_out.dtype != torch.int8 or q8_out.stride() != q.stride()):
         raise ValueError("sage_attn hip: invalid argument: q8_out must be int8 with q's strides")
     rc = lib.sage_attn_fwd_q(
@@ -397,7 +405,7 @@ def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block"
         o = attention(q, k, v, pre, causal, pv_dtype=pv_dtype, q_sub=q_sub, blkq=blkq, blkk=blkk,
                       tensor_layout=tensor_layout)
     if return_intermediates:
-        pre.pop("workspace", None)
-        pre.pop("vt", None)
+        for key in ("workspace", "vt", "vt_pv"):
+            pre.pop(key, None)
         return o, pre
     return o
