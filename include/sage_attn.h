@@ -156,6 +156,33 @@ int sage_prepass_vt(const void* q, const void* k, const void* v, int in_dtype, i
                     void* workspace, size_t workspace_bytes, int pv_mode, void* vtiles,
                     size_t vtile_bytes, void* stream);
 
+/* Bytes of the fixed scratch array that sage_prepass_vt_noalloc uses on each GPU. */
+#define SAGE_SCRATCH_BYTES (4u << 20)
+
+/*
+ * sage_prepass_vt without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * per-chunk K channel sums and V channel maxima live in a scratch array of
+ * SAGE_SCRATCH_BYTES inside the library, one copy per GPU, held until the
+ * process ends; the call allocates nothing.  Problems whose
+ * sage_prepass_workspace_bytes() exceeds SAGE_SCRATCH_BYTES fail with
+ * "invalid argument" (every BASELINE configuration needs at most 1 MiB).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must be serialized by the
+ * caller.  Outputs equal those of sage_prepass_vt.
+ *
+ *  every argument of sage_prepass_vt except workspace and workspace_bytes
+ */
+int sage_prepass_vt_noalloc(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                            int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                            const int64_t* q_strides, const int64_t* k_strides,
+                            const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
+                            int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
+                            float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
+                            float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                            int pv_mode, void* vtiles, size_t vtile_bytes, void* stream);
+
 /*
  * Fused attention: O = softmax2(dequant(Q8 K8^T)) V with an online,
  * base-2 softmax (the log2(e) factor is already folded into q_scale).

@@ -26,7 +26,8 @@ def lib(hip_impl):
 def test_header_declares_the_entry_points():
     assert _declared_functions() == ["sage_abi_version", "sage_attn_fwd", "sage_attn_fwd_q", "sage_flash_fwd",
                                      "sage_last_error", "sage_prepass", "sage_prepass_vt",
-                                     "sage_prepass_workspace_bytes", "sage_vtile_bytes", "sage_vtiles"]
+                                     "sage_prepass_vt_noalloc", "sage_prepass_workspace_bytes",
+                                     "sage_vtile_bytes", "sage_vtiles"]
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -45,6 +46,23 @@ def test_workspace_bytes(lib):
     assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 1, 0) == 4 * 32 * nch * 128 * 4
     assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 1, 1) == 2 * 4 * 32 * nch * 128 * 4
     assert lib.sage_prepass_workspace_bytes(4, 32, 4096, 128, 0, 0) == 0
+
+
+def test_noalloc_prepass_rejects_before_touching_a_device(lib):
+    """The fixed-scratch pre-pass checks its size limit (and a null V tile
+    buffer) before any HIP call."""
+    m = re.search(r"#define SAGE_SCRATCH_BYTES \((\d+)u << (\d+)\)", HEADER.read_text())
+    limit = int(m.group(1)) << int(m.group(2))
+    assert limit == 4 << 20
+    a = _prepass_args(B=16, Hq=64, Hkv=64, Nq=4096, Nkv=4096, D=128, smooth=1, km=ctypes.c_void_p(16))
+    assert lib.sage_prepass_workspace_bytes(16, 64, 4096, 128, 1, 0) > limit
+    fn = lib.sage_prepass_vt_noalloc
+    rc = fn(*a[:-3], 0, ctypes.c_void_p(16), ctypes.c_size_t(1 << 30), None)
+    msg = lib.sage_last_error().decode()
+    assert rc != 0 and "invalid argument" in msg and "scratch" in msg, msg
+    rc = fn(*_prepass_args()[:-3], 0, None, ctypes.c_size_t(0), None)
+    msg = lib.sage_last_error().decode()
+    assert rc != 0 and "invalid argument" in msg and "vtiles" in msg, msg
 
 
 def _prepass_args(**over):

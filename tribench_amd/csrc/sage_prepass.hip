@@ -19,6 +19,7 @@
 // 16-byte loads, held in registers while the block's max|x| is reduced, then
 // quantized and written with 16-byte stores.  Build with -ffp-contract=off:
 // the element arithmetic must round exactly like the reference's.
+#include <mutex>
 #include <type_traits>
 
 #include "sage_device.h"
@@ -674,4 +675,63 @@ extern "C" int sage_prepass_vt(const void* q, const void* k, const void* v, int 
                       v_strides, q_mul, blkq, blkk, q_sub, smooth_k, v_mode, q8, q8_strides, q_scale, k8,
                       k8_strides, k_scale, km, v8, v8_strides, v_scale, workspace, workspace_bytes, pv_mode, vtiles,
                       vtile_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+// sage_prepass_vt_noalloc: sage_prepass_vt with the launch-A partials (K
+// channel sums, V channel maxima) in a fixed scratch array of this library
+// instead of a caller workspace, for callers that cannot allocate device
+// memory.  Each GPU holds its own copy of the array until the process ends.
+// Launch A writes every partial that launch B of the same call reads, so
+// nothing needs clearing between calls; calls that overlap on one GPU race.
+// ---------------------------------------------------------------------------
+namespace sage {
+
+static __device__ __align__(256) char scratch[SAGE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static void* scratch_dev[kMaxDevices];  // device address of `scratch`, per GPU
+static std::mutex scratch_mu;
+
+// The current device's address of `scratch`, looked up once per device with
+// that device current.  In host code the array's name is a host-side stand-in,
+// never a device address: only this pointer may be handed to kernels.
+static int scratch_address(const char* who, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail("%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail("%s: device %d beyond the %d supported", who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail("%s: hipGetSymbolAddress(scratch): %s", who, hipGetErrorString(e));
+    scratch_dev[dev] = p;
+  }
+  *out = scratch_dev[dev];
+  return 0;
+}
+
+}  // namespace sage
+
+extern "C" int sage_prepass_vt_noalloc(const void* q, const void* k, const void* v, int in_dtype, int64_t B,
+                                       int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nkv, int64_t D,
+                                       const int64_t* q_strides, const int64_t* k_strides,
+                                       const int64_t* v_strides, float q_mul, int blkq, int blkk, int q_sub,
+                                       int smooth_k, int v_mode, int8_t* q8, const int64_t* q8_strides,
+                                       float* q_scale, int8_t* k8, const int64_t* k8_strides, float* k_scale,
+                                       float* km, uint8_t* v8, const int64_t* v8_strides, float* v_scale,
+                                       int pv_mode, void* vtiles, size_t vtile_bytes, void* stream) {
+  const char* who = "sage_prepass_vt_noalloc";
+  if (!vtiles) return fail("%s: invalid argument: null pointer (vtiles)", who);
+  const size_t need = sage_prepass_workspace_bytes(B, Hkv, Nkv, D, smooth_k, v_mode);
+  if (need > SAGE_SCRATCH_BYTES)
+    return fail("%s: invalid argument: the problem needs %zu bytes of scratch, the library's fixed scratch "
+                "holds %zu (use sage_prepass_vt with a workspace)",
+                who, need, (size_t)SAGE_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_address(who, &ws)) return rc;
+  return prepass_impl(who, q, k, v, in_dtype, B, Hq, Hkv, Nq, Nkv, D, q_strides, k_strides, v_strides, q_mul,
+                      blkq, blkk, q_sub, smooth_k, v_mode, q8, q8_strides, q_scale, k8, k8_strides, k_scale, km, v8,
+                      v8_strides, v_scale, ws, SAGE_SCRATCH_BYTES, pv_mode, vtiles, vtile_bytes, stream);
 }

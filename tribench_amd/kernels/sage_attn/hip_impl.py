@@ -81,6 +81,8 @@ def _load():
     ]
     lib.sage_prepass_vt.restype = i32
     lib.sage_prepass_vt.argtypes = lib.sage_prepass.argtypes[:-1] + [i32, vp, sz, vp]
+    lib.sage_prepass_vt_noalloc.restype = i32
+    lib.sage_prepass_vt_noalloc.argtypes = lib.sage_prepass.argtypes[:-3] + [i32, vp, sz, vp]
     lib.sage_vtile_bytes.restype = sz
     lib.sage_vtile_bytes.argtypes = [i64, i64, i64, i64, i32]
     lib.sage_vtiles.restype = i32
@@ -189,7 +191,7 @@ def vtiles(v, pv_dtype="fp16", v_scale=None, *, tensor_layout="HND"):
 
 
 def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smooth_k=True,
-            v_fp8=False, pv_dtype=None, quant_q=True, tensor_layout="HND"):
+            v_fp8=False, pv_dtype=None, quant_q=True, tensor_layout="HND", static_scratch=False):
     """Run the HIP pre-pass; returns a dict of device tensors.
 
     q8/k8 (int8, same layout as q/k), q_scale [B,Hq,ceil(Nq/blkq)*(blkq/q_sub)],
@@ -197,6 +199,9 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
     codes as uint8) + v_scale [B,Hkv,D] (v_fp8), and with ``pv_dtype`` the V
     tiles ``vt`` that :func:`attention` reads (v_scale too for "fp8").  With
     ``quant_q=False`` Q is left to :func:`attention_q` (no q8 / q_scale).
+    ``static_scratch=True`` (needs ``pv_dtype``) calls sage_prepass_vt_noalloc,
+    whose partial sums live in the library's fixed per-GPU scratch array
+    instead of a workspace tensor (calls that overlap on one GPU race on it).
     """
     lib = _load()
     B, Hq, Hkv, Nq, Nkv, D = _check_inputs(q, k, v if v is not None else k, tensor_layout)
@@ -219,8 +224,10 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         v_scale = torch.empty((B, Hkv, D), dtype=torch.float32, device=dev)
     if v_fp8:
         v8 = _empty_like_layout(v, torch.uint8)
-    ws_bytes = lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), v_mode)
-    ws = torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
+    if static_scratch and pv_dtype is None:
+        raise ValueError("sage_attn hip: invalid argument: static_scratch needs pv_dtype (sage_prepass_vt_noalloc)")
+    ws_bytes = 0 if static_scratch else lib.sage_prepass_workspace_bytes(B, Hkv, Nkv, D, int(smooth_k), v_mode)
+    ws = None if static_scratch else torch.empty((max(ws_bytes, 1),), dtype=torch.uint8, device=dev)
     uses_v = v_mode != V_NONE or pv_dtype is not None
     args = [
         _ptr(q) if quant_q else None, _ptr(k), _ptr(v) if uses_v else None, _TORCH_CODES[q.dtype], B, Hq, Hkv,
@@ -230,19 +237,25 @@ def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smoot
         _ptr(q8), _strides(q8, tensor_layout) if quant_q else None, _ptr(q_scale), _ptr(k8),
         _strides(k8, tensor_layout),
         _ptr(k_scale), _ptr(km), _ptr(v8), _strides(v8, tensor_layout) if v_fp8 else None, _ptr(v_scale),
-        _ptr(ws), ctypes.c_size_t(ws_bytes),
     ]
     vt = None
     if pv_dtype is None:
-        rc = lib.sage_prepass(*args, _stream(dev))
+        rc = lib.sage_prepass(*args, _ptr(ws), ctypes.c_size_t(ws_bytes), _stream(dev))
         _check(rc, "sage_prepass")
     else:
         # the V tiles of vtiles(), written by the pre-pass's own launches
         nbytes = lib.sage_vtile_bytes(B, Hkv, Nkv, D, PV_MODES[pv_dtype])
         vt = torch.empty((nbytes,), dtype=torch.uint8, device=dev)
-        rc = lib.sage_prepass_vt(*args, PV_MODES[pv_dtype], _ptr(vt), ctypes.c_size_t(nbytes), _stream(dev))
-        _check(rc, "sage_prepass_vt")
-    out = {"k8": k8, "k_scale": k_scale, "workspace": ws}
+        tail = [PV_MODES[pv_dtype], _ptr(vt), ctypes.c_size_t(nbytes), _stream(dev)]
+        if static_scratch:
+            rc = lib.sage_prepass_vt_noalloc(*args, *tail)
+            _check(rc, "sage_prepass_vt_noalloc")
+        else:
+            rc = lib.sage_prepass_vt(*args, _ptr(ws), ctypes.c_size_t(ws_bytes), *tail)
+            _check(rc, "sage_prepass_vt")
+    out = {"k8": k8, "k_scale": k_scale}
+    if ws is not None:
+        out["workspace"] = ws
     if quant_q:
         out["q8"] = q8
         out["q_scale"] = q_scale
