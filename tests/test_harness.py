@@ -1,10 +1,10 @@
-"""The harness around the hot path, on the CPU: schema, registry, case grid,
-inputs, reference, correctness gate, timers, metrics, CLI and outputs.
+"""The harness around the hot path, on the CPU: schema, pack index, case
+grid, inputs, reference, correctness gate, timers, metrics, CLI and outputs.
 
-Schema tests follow the reference's tests/test_meta_schema.py (:12-134); the
-CLI failure handling is forced from the host with fake packs (an impl that
-raises, an impl that returns wrong values), as the reference's CLI handles
-them (cli.py:313-339).
+The schema cases cover what the reference's tests/test_meta_schema.py
+(:12-134) checks of a meta.json; the CLI failure handling is forced from the
+host with fake packs (an impl that raises, an impl that returns wrong
+values), as the reference's CLI handles them (cli.py:313-339).
 """
 from __future__ import annotations
 
@@ -21,12 +21,14 @@ import torch
 from oracle import sage_oracle as O
 from tribench_amd.harness import bench as hb
 from tribench_amd.harness import cli
+from tribench_amd.harness import schema, stats
+from tribench_amd.harness.cases import Case, case_grid, seeded_inputs
 from tribench_amd.harness.correctness import _get_tolerance, check_correctness
-from tribench_amd.harness.gen import generate_cases, materialize_inputs
-from tribench_amd.harness.meta import load_meta, validate_entrypoints, validate_meta
 from tribench_amd.harness.metrics import PEAKS_MI355X, compute_gbps, compute_tflops, roofline_fraction
-from tribench_amd.harness.registry import KernelRegistry
+from tribench_amd.harness.packs import PackIndex
 from tribench_amd.harness.types import CorrectnessSpec
+
+PACKS = Path(__file__).resolve().parents[1] / "tribench_amd" / "kernels"
 
 VALID_META = {
     "schema_version": "1.0",
@@ -34,7 +36,7 @@ VALID_META = {
     "family": "test",
     "description": "A test kernel",
     "entrypoints": {"make_inputs": "reference.py:make_inputs", "reference": "reference.py:ref",
-                    "variants": {"hip": "impl.py:run"}},
+                    "triton": "impl.py:run", "variants": {"hip": "impl.py:run"}},
     "supported": {"dtypes": ["fp16", "bf16"], "layouts": ["contiguous"], "backends": ["hip"]},
     "cases": [{"name": "small", "N": 16}],
 }
@@ -45,7 +47,7 @@ VALID_META = {
 # ---------------------------------------------------------------------------
 
 def test_valid_meta_passes():
-    assert validate_meta(VALID_META) == []
+    assert schema.check(VALID_META) == []
 
 
 @pytest.mark.parametrize("field", ["schema_version", "name", "family", "description", "entrypoints", "supported",
@@ -53,46 +55,80 @@ def test_valid_meta_passes():
 def test_missing_top_field(field):
     m = copy.deepcopy(VALID_META)
     del m[field]
-    assert any(field in e for e in validate_meta(m))
+    assert any(f"'{field}' is required" in e for e in schema.check(m))
 
 
 @pytest.mark.parametrize("path,value,needle", [
-    (("supported", "dtypes"), ["fp8"], "Invalid dtype"),
-    (("supported", "layouts"), ["strided"], "Invalid layout"),
-    (("supported", "backends"), ["metal"], "Invalid backend"),
-    (("entrypoints", "variants"), ["x"], "must be a dict"),
+    (("supported", "dtypes"), ["fp8"], "supported.dtypes: 'fp8'"),
+    (("supported", "layouts"), ["strided"], "supported.layouts: 'strided'"),
+    (("supported", "backends"), ["metal"], "supported.backends: 'metal'"),
+    (("entrypoints", "variants"), ["x"], "variants must map"),
+    (("entrypoints", "reference"), "reference.py", "not of the form"),
+    (("entrypoints", "estimate"), "reference.py:1x", "not of the form"),
 ])
 def test_bad_values(path, value, needle):
     m = copy.deepcopy(VALID_META)
     m[path[0]][path[1]] = value
-    assert any(needle in e for e in validate_meta(m))
+    assert any(needle in e for e in schema.check(m))
 
 
-def test_case_without_name_and_bad_schema_version():
+def test_case_names_and_field_types():
     m = copy.deepcopy(VALID_META)
-    m["cases"] = [{"N": 3}]
+    m["cases"] = [{"N": 3}, {"name": "a"}, {"name": "a"}]
     m["schema_version"] = 1
-    errs = validate_meta(m)
-    assert any("missing 'name'" in e for e in errs) and any("must be a string" in e for e in errs)
+    errs = schema.check(m)
+    assert any("cases[0] needs a 'name'" in e for e in errs)
+    assert any("'a' is used twice" in e for e in errs)
+    assert any("'schema_version' must be a str" in e for e in errs)
 
 
-def test_pack_needs_an_implementation():
-    m = copy.deepcopy(VALID_META)
-    m["entrypoints"].pop("variants")
-    assert any("No implementation" in e for e in validate_meta(m))
-    m["entrypoints"]["triton"] = "impl.py:run"  # a reference-style main entrypoint also counts
-    assert validate_meta(m) == []
+def test_triton_entrypoint_is_required():
+    """TriBench's validator requires make_inputs, reference and triton
+    (tribench/meta.py:29); so does this one, so the packs pass both."""
+    for role in ("make_inputs", "reference", "triton"):
+        m = copy.deepcopy(VALID_META)
+        m["entrypoints"].pop(role)
+        assert any(f"'{role}' is required" in e for e in schema.check(m))
+
+
+@pytest.mark.parametrize("pack", ["sage_attn", "flash_attn"])
+def test_packs_satisfy_the_reference_required_fields(pack):
+    """Each committed meta.json has every field TriBench's validate-meta
+    requires (top level and entrypoints, tribench/meta.py:24-29), its
+    entrypoint files exist, and its triton slot is the HIP variant."""
+    raw = json.loads((PACKS / pack / "meta.json").read_text())
+    assert {"schema_version", "name", "family", "description", "entrypoints", "supported", "cases"} <= set(raw)
+    assert {"make_inputs", "reference", "triton"} <= set(raw["entrypoints"])
+    assert raw["entrypoints"]["triton"] == raw["entrypoints"]["variants"]["hip"] == "hip_impl.py:run"
+    assert schema.check(raw, PACKS / pack) == []
 
 
 def test_sage_pack_meta_and_entrypoints():
-    reg = KernelRegistry()
-    assert "sage_attn" in reg.kernel_names()
-    assert reg.validate_all() == {}
-    meta = reg.get_meta("sage_attn")
+    index = PackIndex()
+    assert "sage_attn" in index.names()
+    assert index.problems() == {}
+    meta = index.pack("sage_attn").meta
     assert meta.entrypoints.variants == {"hip": "hip_impl.py:run"}
-    assert validate_entrypoints(meta) == []
     names = [c.name for c in meta.cases]
     assert {"s4k_d64", "s8k_d64", "cfg1_b1h2n256d64", "cfg2_b4h32n4096d128"} <= set(names)
+
+
+def test_index_reports_a_broken_pack_and_keeps_the_others(tmp_path):
+    good = tmp_path / "good"
+    good.mkdir()
+    m = copy.deepcopy(VALID_META)
+    m["name"] = "good"
+    (good / "meta.json").write_text(json.dumps(m))
+    for f in ("reference.py", "impl.py"):
+        (good / f).write_text("")
+    bad = tmp_path / "bad"
+    bad.mkdir()
+    (bad / "meta.json").write_text("{not json")
+    index = PackIndex(tmp_path)
+    assert index.names() == ["good"]
+    assert list(index.problems()) == [str(bad / "meta.json")]
+    with pytest.raises(KeyError, match="no kernel pack 'nope'"):
+        index.pack("nope")
 
 
 def test_flash_pack_meta_entrypoints_and_shared_reference():
@@ -104,16 +140,16 @@ def test_flash_pack_meta_entrypoints_and_shared_reference():
 
     from oracle import sage_oracle as O
 
-    reg = KernelRegistry()
-    meta = reg.get_meta("flash_attn")
+    pack = PackIndex().pack("flash_attn")
+    meta = pack.meta
     assert meta.entrypoints.variants == {"hip": "hip_impl.py:run"}
-    assert validate_entrypoints(meta) == []
     assert {"s4k_d64", "s8k_d64"} <= {c.name for c in meta.cases}
-    ref_mod = reg.load_symbol("flash_attn", "reference.py:ref").__module__
+    ref_mod = pack.resolve("reference.py:ref").__module__
     assert ref_mod == "tribench.kernels.flash_attn.reference"
-    make = reg.load_symbol("flash_attn", "reference.py:make_inputs")
-    ref = reg.load_symbol("flash_attn", "reference.py:ref")
-    est = reg.load_symbol("flash_attn", "reference.py:estimate")
+    make = pack.entry("make_inputs")
+    ref = pack.entry("reference")
+    est = pack.entry("estimate")
+    assert ref is pack.resolve("reference.py:ref")  # one import per file
     case = dict(batch_size=1, num_heads=2, seq_len=70, head_dim=64, causal=True)
     inp = make(case, "cpu", 0, torch.float16)
     assert inp["q"].dtype == torch.float16 and inp["q"].shape == (1, 2, 70, 64) and inp["causal"]
@@ -125,34 +161,47 @@ def test_flash_pack_meta_entrypoints_and_shared_reference():
 
 
 # ---------------------------------------------------------------------------
-# registry / case grid / inputs / reference / estimate
+# pack index / case grid / inputs / reference / estimate
 # ---------------------------------------------------------------------------
 
-def test_registry_loads_by_file_path_without_a_parent_package():
-    reg = KernelRegistry()
-    impls = reg.implementations("sage_attn")
-    assert [n for n, _ in impls] == ["hip"]
+def test_pack_loads_by_file_path_without_a_parent_package():
+    import sys
+
+    pack = PackIndex().pack("sage_attn")
+    impls = pack.implementations()
+    assert [n for n, _ in impls] == ["hip"]  # the triton slot names the same function: listed once
     fn = impls[0][1]
     assert fn.__module__ == "tribench.kernels.sage_attn.hip_impl"
+    assert "tribench.kernels.sage_attn" not in sys.modules and "tribench" not in sys.modules
+    assert pack.entry("triton") is pack.variant("hip")
+    with pytest.raises(KeyError, match="no variant 'cuda'"):
+        pack.variant("cuda")
 
 
-def test_generate_cases_grid_and_filters():
-    meta = KernelRegistry().get_meta("sage_attn")
-    grid = generate_cases(meta, case_filter=["cfg2_b4h32n4096d128"], dtype_filter=["bf16"])
-    assert len(grid) == 1 and grid[0]["params"]["head_dim"] == 128 and grid[0]["dtype"] == "bf16"
-    assert len(generate_cases(meta)) == len(meta.cases) * 3
-    with pytest.raises(ValueError, match="does not support dtype"):
-        generate_cases(meta, dtype_filter=["fp64"])
-    with pytest.raises(ValueError, match="no case"):
-        generate_cases(meta, case_filter=["nope"])
+def test_case_grid_and_filters():
+    meta = PackIndex().pack("sage_attn").meta
+    grid = case_grid(meta, cases=["cfg2_b4h32n4096d128"], dtypes=["bf16"])
+    assert grid == [Case("cfg2_b4h32n4096d128", dict(meta.cases[3].params), "bf16", "contiguous")]
+    assert grid[0].params["head_dim"] == 128
+    assert len(case_grid(meta)) == len(meta.cases) * 3
+    assert [c.dtype for c in case_grid(meta, cases=["s4k_d64"], dtypes=["fp32", "bf16", "fp32"])] == ["fp32", "bf16"]
+    with pytest.raises(ValueError, match="no dtype 'fp64'"):
+        case_grid(meta, dtypes=["fp64"])
+    with pytest.raises(ValueError, match="no case 'nope'"):
+        case_grid(meta, cases=["nope"])
 
 
-def test_materialize_inputs_is_seeded(pack_ref):
-    case = {"case_name": "c", "params": dict(batch_size=1, num_heads=2, num_kv_heads=1, seq_len=40, head_dim=64,
-                                             k_offset_std=2.0), "dtype": "bf16", "layout": "contiguous"}
-    a = materialize_inputs(pack_ref.make_inputs, case, "cpu", 0)
-    b = materialize_inputs(pack_ref.make_inputs, case, "cpu", 0)
-    c = materialize_inputs(pack_ref.make_inputs, case, "cpu", 1)
+def test_seeded_inputs(pack_ref):
+    case = Case("c", dict(batch_size=1, num_heads=2, num_kv_heads=1, seq_len=40, head_dim=64, k_offset_std=2.0),
+                "bf16", "contiguous")
+    a = seeded_inputs(pack_ref.make_inputs, case, "cpu", 0)
+    b = seeded_inputs(pack_ref.make_inputs, case, "cpu", 0)
+    c = seeded_inputs(pack_ref.make_inputs, case, "cpu", 1)
+    # the global generator is seeded before make_inputs (a pack drawing from it is reproducible)
+    draw = lambda params, device, seed, dtype: {"x": torch.rand(3, dtype=dtype)}  # noqa: E731
+    x1 = seeded_inputs(draw, Case("d", {}, "fp32", "contiguous"), "cpu", 5)["x"]
+    x2 = seeded_inputs(draw, Case("d", {}, "fp32", "contiguous"), "cpu", 5)["x"]
+    assert torch.equal(x1, x2)
     assert all(torch.equal(a[x], b[x]) for x in "qkv") and not torch.equal(a["q"], c["q"])
     assert a["q"].shape == (1, 2, 40, 64) and a["k"].shape == (1, 1, 40, 64) and a["q"].dtype == torch.bfloat16
 
@@ -213,15 +262,17 @@ def test_per_case_tolerance_overrides():
     assert not check_correctness(ref, one_big, "bf16", spec).passed
     m = copy.deepcopy(VALID_META)
     m["correctness"] = {"atol": 5e-2, "per_case": {"small": {"atol": 1.0}}}
-    assert validate_meta(m) == []
+    assert schema.check(m) == []
     m["correctness"]["per_case"] = {"nope": {"atol": 1.0}}
-    assert any("unknown case" in e for e in validate_meta(m))
+    assert any("no case named 'nope'" in e for e in schema.check(m))
     m["correctness"]["per_case"] = {"small": {"tol": 1.0}}
-    assert any("takes atol" in e for e in validate_meta(m))
+    assert any("allowed keys are" in e for e in schema.check(m))
+    m["correctness"] = {"atol": "big"}
+    assert any("correctness.atol must be a number" in e for e in schema.check(m))
 
 
 def test_sage_pack_fp8_case_gate():
-    meta = load_meta(Path(KernelRegistry().get_meta("sage_attn").kernel_dir) / "meta.json")
+    meta = schema.read(PACKS / "sage_attn" / "meta.json")
     c5 = meta.correctness.for_case("cfg5_fp8pv_b1h32n32768d128")
     assert (c5.atol, c5.rtol, c5.min_cos) == (2.0, 5e-2, 0.999)
     assert meta.correctness.for_case("cfg2_b4h32n4096d128").atol == 5e-2
@@ -281,7 +332,7 @@ def _fake_pack(root: Path, impl_body: str) -> Path:
 ])
 def test_cli_test_on_fake_packs(tmp_path, monkeypatch, capsys, body, code, needle):
     kdir = _fake_pack(tmp_path, body)
-    monkeypatch.setattr("tribench_amd.harness.registry._DEFAULT_KERNELS_DIR", kdir)
+    monkeypatch.setattr("tribench_amd.harness.packs.KERNELS_DIR", kdir)
     with pytest.raises(SystemExit) as e:
         cli.main(["test", "--kernel", "fake", "--device", "cpu"])
     out = capsys.readouterr().out
@@ -298,7 +349,7 @@ def test_cli_test_hip_variant_without_gpu_fails_loudly(capsys):
 
 def test_cli_run_writes_results(tmp_path, monkeypatch, capsys):
     kdir = _fake_pack(tmp_path, "def run(x):\n    return x * 2\n")
-    monkeypatch.setattr("tribench_amd.harness.registry._DEFAULT_KERNELS_DIR", kdir)
+    monkeypatch.setattr("tribench_amd.harness.packs.KERNELS_DIR", kdir)
     with pytest.raises(SystemExit) as e:
         cli.main(["run", "--kernel", "fake", "--device", "cpu", "--timer", "cpu_wall", "--warmup-ms", "1",
                   "--rep-ms", "5", "--output-dir", str(tmp_path / "res"), "--cpu-ref"])
@@ -358,14 +409,33 @@ def test_cli_list_and_validate(capsys):
 
 def test_cpu_timer_and_stats():
     lats = hb._bench_cpu_wall(lambda: math.sqrt(2.0), 1.0, 2.0)
-    st = hb._stats(lats)
-    assert len(lats) >= 1 and st["p50"] >= 0 and st["p99"] >= st["p50"]
+    st = stats.summarize(lats)
+    assert len(lats) >= 1 and st.p50 >= 0 and st.p99 >= st.p50
     threads, model = hb.cpu_info()
     assert threads >= 1 and isinstance(model, str)
+    s = stats.summarize([1.0, 1.0, 1.0, 5.0])
+    assert s.p50 == 1.0 and s.tail == pytest.approx(s.p99) and s.jitter == pytest.approx(s.std / 2.0)
+    assert stats.summarize([0.0]).tail is None
+    with pytest.raises(ValueError):
+        stats.summarize([])
+
+
+def test_workload_and_rates():
+    attn = stats.workload(dict(batch_size=4, num_heads=32, num_kv_heads=8, seq_len=4096, head_dim=128))
+    assert attn == stats.Workload(tokens=4 * 4096, elements=4 * 32 * 4096 * 128, sequences=4)
+    assert stats.workload(dict(M=64, N=32)) == stats.Workload(elements=64 * 32)
+    assert stats.workload(dict(seq_len=10)) == stats.Workload(tokens=10, elements=10)
+    assert stats.workload(dict(flag=True, name="x")) == stats.Workload()
+    r = stats.rates(attn, 2.0)
+    assert r["tokens_per_s"] == 4 * 4096 * 500 and r["sequences_per_s"] == 2000
+    assert stats.rates(attn, 0.0)["elements_per_s"] is None
+    with stats.PeakMemory("cpu") as mem:
+        pass
+    assert mem.allocated_mib is None and mem.reserved_mib is None
 
 
 def test_load_meta_keeps_case_params():
-    meta = load_meta(Path(KernelRegistry().get_meta("sage_attn").kernel_dir) / "meta.json")
+    meta = schema.read(PACKS / "sage_attn" / "meta.json")
     c = {x.name: x.params for x in meta.cases}["cfg5_fp8pv_b1h32n32768d128"]
     assert c["pv_dtype"] == "fp8" and c["q_gran"] == "wave" and "name" not in c
 
@@ -373,7 +443,8 @@ def test_load_meta_keeps_case_params():
 def test_roofline_unit_per_pack():
     from tribench_amd.harness.cli import roofline_unit_for
 
-    reg = KernelRegistry()
-    assert roofline_unit_for(reg.get_meta("sage_attn"), {"dtype": "bf16"}) == "int8"
-    assert roofline_unit_for(reg.get_meta("flash_attn"), {"dtype": "fp16"}) == "fp16"
-    assert roofline_unit_for(reg.get_meta("flash_attn"), {"dtype": "bf16"}) == "bf16"
+    index = PackIndex()
+    case = lambda dt: Case("c", {}, dt, "contiguous")  # noqa: E731
+    assert roofline_unit_for(index.pack("sage_attn").meta, case("bf16")) == "int8"
+    assert roofline_unit_for(index.pack("flash_attn").meta, case("fp16")) == "fp16"
+    assert roofline_unit_for(index.pack("flash_attn").meta, case("bf16")) == "bf16"

@@ -21,15 +21,13 @@ from __future__ import annotations
 import os
 import platform
 import time
-from typing import Any, Callable
+from typing import Callable
 
-import numpy as np
 import torch
 
+from . import stats
+from .cases import Case, seeded_inputs
 from .correctness import check_correctness
-from .eval_metrics import (compute_domain_throughputs, compute_jitter_cv, compute_tail_ratio,
-                           read_peak_memory_mb, reset_peak_memory_stats)
-from .gen import materialize_inputs
 from .metrics import PEAKS_MI355X, compute_gbps, compute_tflops, get_estimate_dict
 from .types import BenchResult, CorrectnessResult, KernelMeta
 
@@ -118,15 +116,6 @@ def cpu_info() -> tuple[int, str]:
     return threads, model
 
 
-def _stats(lats: list[float]) -> dict[str, float]:
-    a = np.asarray(lats, dtype=np.float64)
-    return {
-        "p50": float(np.percentile(a, 50)), "p90": float(np.percentile(a, 90)),
-        "p95": float(np.percentile(a, 95)), "p99": float(np.percentile(a, 99)),
-        "min": float(a.min()), "max": float(a.max()), "mean": float(a.mean()), "std": float(a.std()),
-    }
-
-
 def run_benchmark(
     *,
     kernel_name: str,
@@ -135,7 +124,7 @@ def run_benchmark(
     reference_fn: Callable,
     triton_fn: Callable,
     estimate_fn: Callable | None,
-    case: dict[str, Any],
+    case: Case,
     device: str,
     seed: int,
     warmup_ms: float = 200.0,
@@ -158,30 +147,27 @@ def run_benchmark(
     if timer_backend != "cpu_wall" and not device.startswith("cuda"):
         timer_backend = "cpu_wall"
     timer = TIMER_BACKENDS[timer_backend]
-    dtype_str = case["dtype"]
-    reset_peak_memory_stats(device)
-    inputs = materialize_inputs(make_inputs_fn, case, device, seed)
+    with stats.PeakMemory(device) as mem:
+        inputs = seeded_inputs(make_inputs_fn, case, device, seed)
 
-    t0 = time.perf_counter()
-    _ = triton_fn(**inputs)
-    _sync(device)
-    compile_time_ms = (time.perf_counter() - t0) * 1e3
-
-    corr: CorrectnessResult | None = None
-    if run_correctness:
-        ref_out = reference_fn(**inputs)
-        out = triton_fn(**inputs)
+        t0 = time.perf_counter()
+        _ = triton_fn(**inputs)
         _sync(device)
-        corr = check_correctness(ref_out, out, dtype_str, meta.correctness.for_case(case["case_name"]))
-        del ref_out, out
+        compile_time_ms = (time.perf_counter() - t0) * 1e3
 
-    lats = timer(lambda: triton_fn(**inputs), warmup_ms, rep_ms)
-    st = _stats(lats)
-    p50 = st["p50"]
-    domain = compute_domain_throughputs(case["params"], p50)
-    alloc_mb, reserved_mb = read_peak_memory_mb(device)
+        corr: CorrectnessResult | None = None
+        if run_correctness:
+            ref_out = reference_fn(**inputs)
+            out = triton_fn(**inputs)
+            _sync(device)
+            corr = check_correctness(ref_out, out, case.dtype, meta.correctness.for_case(case.name))
+            del ref_out, out
 
-    est = get_estimate_dict(estimate_fn, case["params"])
+        st = stats.summarize(timer(lambda: triton_fn(**inputs), warmup_ms, rep_ms))
+    p50 = st.p50
+    per_s = stats.rates(stats.workload(case.params), p50)
+
+    est = get_estimate_dict(estimate_fn, case.params)
     flops, bytes_ = est.get("flops"), est.get("bytes")
     tflops = compute_tflops(flops, p50) if flops else None
     gbps = compute_gbps(bytes_, p50) if bytes_ else None
@@ -189,13 +175,12 @@ def run_benchmark(
     peak = PEAKS_MI355X.get(roofline_unit)
 
     res = BenchResult(
-        kernel=kernel_name, case_name=case["case_name"], dtype=dtype_str, layout=case["layout"],
-        latency_ms_p50=p50, latency_ms_p90=st["p90"], latency_ms_p95=st["p95"], latency_ms_p99=st["p99"],
-        latency_ms_min=st["min"], latency_ms_max=st["max"], latency_ms_mean=st["mean"],
-        latency_ms_std=st["std"], pass_type=pass_type, tflops=tflops, gbps=gbps,
-        tail_ratio_p99_p50=compute_tail_ratio(st["p99"], p50), jitter_cv=compute_jitter_cv(st["std"], st["mean"]),
-        tokens_per_s=domain.tokens_per_s, elements_per_s=domain.elements_per_s,
-        sequences_per_s=domain.sequences_per_s, peak_mem_alloc_mb=alloc_mb, peak_mem_reserved_mb=reserved_mb,
+        kernel=kernel_name, case_name=case.name, dtype=case.dtype, layout=case.layout,
+        latency_ms_p50=p50, latency_ms_p90=st.p90, latency_ms_p95=st.p95, latency_ms_p99=st.p99,
+        latency_ms_min=st.min, latency_ms_max=st.max, latency_ms_mean=st.mean,
+        latency_ms_std=st.std, pass_type=pass_type, tflops=tflops, gbps=gbps,
+        tail_ratio_p99_p50=st.tail, jitter_cv=st.jitter, **per_s,
+        peak_mem_alloc_mb=mem.allocated_mib, peak_mem_reserved_mb=mem.reserved_mib,
         timer_backend=timer_backend, warmup_ms=warmup_ms, rep_ms=rep_ms, correctness=corr,
         compile_time_ms=compile_time_ms,
         effective_tops=tflops,
@@ -208,8 +193,7 @@ def run_benchmark(
     res.roofline_fraction = (rate / peak) if (rate and peak) else None
     pre_fn = (stage_fns or {}).get("prepass")
     if pre_fn is not None and device.startswith("cuda"):
-        pre_lats = timer(lambda: pre_fn(**inputs), warmup_ms / 4, rep_ms / 4)
-        pre_p50 = _stats(pre_lats)["p50"]
+        pre_p50 = stats.summarize(timer(lambda: pre_fn(**inputs), warmup_ms / 4, rep_ms / 4)).p50
         res.prepass_ms_p50 = pre_p50
         pb = est.get("prepass_bytes")
         if pb and est.get("vtile_bytes"):
@@ -226,7 +210,7 @@ def run_cpu_reference(
     make_inputs_fn: Callable,
     reference_fn: Callable,
     estimate_fn: Callable | None,
-    case: dict[str, Any],
+    case: Case,
     seed: int,
     reps: int = 3,
     max_rep_s: float = 30.0,
@@ -235,7 +219,7 @@ def run_cpu_reference(
     a single rep when one rep exceeds ``max_rep_s``)."""
     threads, model = cpu_info()
     torch.set_num_threads(threads)
-    inputs = materialize_inputs(make_inputs_fn, case, "cpu", seed)
+    inputs = seeded_inputs(make_inputs_fn, case, "cpu", seed)
     times: list[float] = []
     for i in range(reps):
         t0 = time.perf_counter()
@@ -244,14 +228,14 @@ def run_cpu_reference(
         times.append(dt * 1e3)
         if dt > max_rep_s:
             break
-    st = _stats(times)
-    est = get_estimate_dict(estimate_fn, case["params"])
+    st = stats.summarize(times)
+    est = get_estimate_dict(estimate_fn, case.params)
     flops = est.get("flops")
-    tflops = compute_tflops(flops, st["p50"]) if flops else None
+    tflops = compute_tflops(flops, st.p50) if flops else None
     return BenchResult(
-        kernel=kernel_name, case_name=case["case_name"], dtype=case["dtype"], layout=case["layout"],
-        latency_ms_p50=st["p50"], latency_ms_p90=st["p90"], latency_ms_p95=st["p95"], latency_ms_p99=st["p99"],
-        latency_ms_min=st["min"], latency_ms_max=st["max"], latency_ms_mean=st["mean"],
-        latency_ms_std=st["std"], variant="cpu_ref", tflops=tflops, effective_tops=tflops,
+        kernel=kernel_name, case_name=case.name, dtype=case.dtype, layout=case.layout,
+        latency_ms_p50=st.p50, latency_ms_p90=st.p90, latency_ms_p95=st.p95, latency_ms_p99=st.p99,
+        latency_ms_min=st.min, latency_ms_max=st.max, latency_ms_mean=st.mean,
+        latency_ms_std=st.std, variant="cpu_ref", tflops=tflops, effective_tops=tflops,
         timer_backend="cpu_wall", warmup_ms=0.0, rep_ms=0.0, cpu_threads=threads, cpu_model=model,
     )

@@ -63,7 +63,7 @@ def roofline_unit_for(meta, case) -> str:
     quantized QK product dominates), else the case's dtype."""
     if "int8" in (getattr(meta, "tags", None) or []):
         return "int8"
-    return case.get("dtype", "bf16") if case.get("dtype") in ("fp16", "bf16", "fp32") else "bf16"
+    return case.dtype if case.dtype in ("fp16", "bf16", "fp32") else "bf16"
 
 
 def _print_error(prefix: str, e: Exception) -> None:
@@ -97,47 +97,54 @@ def _sync(device: str) -> None:
 
 
 def _cmd_list(args) -> int:
-    from .registry import KernelRegistry
+    from .packs import PackIndex
 
-    reg = KernelRegistry()
-    for m in reg.list_kernels():
-        impls = (["triton"] if m.entrypoints.triton else []) + list(m.entrypoints.variants)
+    index = PackIndex()
+    for name in index.names():
+        pack = index.pack(name)
+        m = pack.meta
+        impls = [label for label, spec in [("triton", m.entrypoints.triton), *m.entrypoints.variants.items()]
+                 if spec]
         print(f"{m.name:20s} {m.family:12s} dtypes={','.join(m.supported.dtypes)} impls={','.join(impls)} "
               f"cases={','.join(c.name for c in m.cases)}")
+    for path, msg in index.broken.items():
+        print(f"(not loaded) {path}: {msg}")
     return 0
 
 
 def _cmd_validate_meta(args) -> int:
-    from .registry import KernelRegistry
+    from .packs import PackIndex
 
-    report = KernelRegistry().validate_all()
-    if not report:
-        print("All meta.json files are valid.")
+    index = PackIndex()
+    problems = index.problems()
+    if not problems:
+        print(f"All meta.json files are valid ({len(index.names())} pack(s)).")
         return 0
-    for name, errors in report.items():
-        print(f"{name}:")
+    for path, errors in problems.items():
+        print(f"{path}:")
         for e in errors:
             print(f"   - {e}")
     return 1
 
 
 def _cmd_test(args) -> int:
+    from .cases import case_grid, seeded_inputs
     from .correctness import check_correctness
-    from .gen import generate_cases, materialize_inputs
-    from .registry import KernelRegistry
+    from .packs import PackIndex
 
-    reg = KernelRegistry()
-    names = reg.kernel_names() if args.kernel == "all" else [n.strip() for n in args.kernel.split(",")]
+    index = PackIndex()
+    names = index.names() if args.kernel == "all" else [n.strip() for n in args.kernel.split(",")]
     dtype_filter = args.dtype.split(",") if args.dtype else None
     case_filter = args.cases.split(",") if args.cases else None
     all_passed = True
     for name in names:
         try:
-            meta = reg.get_meta(name)
-            cases = generate_cases(meta, case_filter=case_filter, dtype_filter=dtype_filter)
-            make_inputs = reg.load_make_inputs(name)
-            reference = reg.load_reference(name)
-            impls = reg.implementations(name)
+            pack = index.pack(name)
+            meta = pack.meta
+            cases = case_grid(meta, cases=case_filter, dtypes=dtype_filter)
+            make_inputs = pack.entry("make_inputs")
+            reference = pack.entry("reference")
+            impls = pack.implementations()
         except Exception as e:
             all_passed = False
             print(f"\n--- {name} ---\n  SKIP  kernel initialization failed")
@@ -146,11 +153,11 @@ def _cmd_test(args) -> int:
         print(f"\n--- {name} ({len(cases)} case(s)) ---")
         for case in cases:
             try:
-                inputs = materialize_inputs(make_inputs, case, args.device, args.seed)
+                inputs = seeded_inputs(make_inputs, case, args.device, args.seed)
                 ref_out = reference(**inputs)
             except Exception as e:
                 all_passed = False
-                print(f"    SKIP  {case['case_name']} dtype={case['dtype']}  (setup/reference exception)")
+                print(f"    SKIP  {case.label()}  (setup/reference exception)")
                 _print_error("     ", e)
                 _clear_device_cache()
                 continue
@@ -159,10 +166,10 @@ def _cmd_test(args) -> int:
                 try:
                     out = fn(**inputs)
                     _sync(args.device)
-                    res = check_correctness(ref_out, out, case["dtype"], meta.correctness.for_case(case["case_name"]))
+                    res = check_correctness(ref_out, out, case.dtype, meta.correctness.for_case(case.name))
                     status = "PASS" if res.passed else "FAIL"
                     cos = "" if res.cosine is None else f"  cos={res.cosine:.6f}"
-                    print(f"    {status}  {case['case_name']} [{label}] dtype={case['dtype']}  "
+                    print(f"    {status}  {case.name} [{label}] dtype={case.dtype}  "
                           f"max_abs={res.max_abs_err:.2e}  max_rel={res.max_rel_err:.2e}{cos}")
                     if not res.passed:
                         all_passed = False
@@ -170,7 +177,7 @@ def _cmd_test(args) -> int:
                             print(f"     {res.error_msg}")
                 except Exception as e:
                     all_passed = False
-                    print(f"    FAIL  {case['case_name']} [{label}] dtype={case['dtype']}  (Exception)")
+                    print(f"    FAIL  {case.name} [{label}] dtype={case.dtype}  (Exception)")
                     _print_error("     ", e)
                     _clear_device_cache()
             del inputs, ref_out
@@ -180,14 +187,14 @@ def _cmd_test(args) -> int:
 
 def _cmd_run(args) -> int:
     from .bench import run_benchmark, run_cpu_reference
+    from .cases import case_grid
     from .env import capture_env
-    from .gen import generate_cases
     from .io import make_run_id, write_json, write_summary_md
-    from .registry import KernelRegistry
+    from .packs import PackIndex
     from .types import RunRecord
 
-    reg = KernelRegistry()
-    names = reg.kernel_names() if args.kernel == "all" else [n.strip() for n in args.kernel.split(",")]
+    index = PackIndex()
+    names = index.names() if args.kernel == "all" else [n.strip() for n in args.kernel.split(",")]
     dtype_filter = args.dtype.split(",") if args.dtype else None
     case_filter = args.cases.split(",") if args.cases else None
     layout_filter = args.layout.split(",") if args.layout else None
@@ -198,13 +205,13 @@ def _cmd_run(args) -> int:
     failed = False
     for name in names:
         try:
-            meta = reg.get_meta(name)
-            cases = generate_cases(meta, case_filter=case_filter, dtype_filter=dtype_filter,
-                                   layout_filter=layout_filter)
-            make_inputs = reg.load_make_inputs(name)
-            reference = reg.load_reference(name)
-            estimate = reg.load_estimate(name)
-            impls = reg.implementations(name)
+            pack = index.pack(name)
+            meta = pack.meta
+            cases = case_grid(meta, cases=case_filter, dtypes=dtype_filter, layouts=layout_filter)
+            make_inputs = pack.entry("make_inputs")
+            reference = pack.entry("reference")
+            estimate = pack.entry("estimate")
+            impls = pack.implementations()
             stage_mod = sys.modules.get(f"tribench.kernels.{name}.hip_impl")
         except Exception as e:
             failed = True
@@ -227,7 +234,7 @@ def _cmd_run(args) -> int:
                                         roofline_unit=roofline_unit_for(meta, case))
                 except Exception as e:
                     failed = True
-                    print(f"    SKIP  {case['case_name']} [{impl_name}] dtype={case['dtype']}  (benchmark exception)")
+                    print(f"    SKIP  {case.name} [{impl_name}] dtype={case.dtype}  (benchmark exception)")
                     _print_error("     ", e)
                     _clear_device_cache()
                     if args.kernel != "all":
