@@ -12,9 +12,12 @@ effective TOPS = 4*B*H*N^2*D / t.  ``roofline`` is the attention kernel's
 algorithmic rate (HIP events around its launches, on its stream) against the
 MI355X dense INT8 MFMA peak; ``cpu_baseline`` times the CPU oracle's fp32
 SDPA (a restatement of reference.py:ref) on a bounded sample of the same
-workload on this host's cores.
+workload on this host's cores.  The metric is quoted at N = 4096 and 16384:
+after the headline configuration the same run times configuration 3 (B=2,
+H=32, N=16384, causal) and reports it as the nested ``n16384`` object, with
+its own step time, effective and algorithmic TOPS and roofline.
 
-  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2]
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2] [--also cfg3|none]
                   [--no-cpu-baseline] [--copy-probe-gib G] [--q-quant auto|prologue|pre-pass]
 """
 from __future__ import annotations
@@ -60,12 +63,28 @@ def _load(stem: str):
 
 
 def _traffic_from_profiles(cfg: str):
-    """HBM bytes per attention launch measured with rocprofv3 (committed summary)."""
+    """HBM bytes per attention launch of a configuration, measured with
+    rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary of that
+    configuration; None if there is none)."""
     f = ROOT / "profiles" / f"attn_fwd_{cfg}_hbm_traffic.md"
     if not f.exists():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
     return float(m.group(1)) if m else None
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 def cpu_baseline(R, case, budget_s: float = 15.0) -> dict:
@@ -98,7 +117,7 @@ def cpu_baseline(R, case, budget_s: float = 15.0) -> dict:
         limiter.unregister()
     ops = 4.0 * heads * N * N * D
     return {
-        "value": ops / dt / 1e12, "unit": "TOPS", "cores": threads, "kind": "port",
+        "value": ops / dt / 1e12, "unit": "TOPS", "cores": threads, "cpu_model": cpu_model(), "kind": "port",
         "sample": f"oracle.sdpa fp32 (numpy BLAS) on {heads} (batch, head) slices of the {B * Hq} "
                   f"(cycled), N={N} D={D}{' causal' if causal else ''}: {dt:.1f} s",
     }
@@ -110,6 +129,9 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--also", default="cfg3", choices=sorted(CONFIGS) + ["none"],
+                    help="a second configuration timed in the same run and reported as a nested object "
+                         "keyed by its sequence length (default cfg3: the metric's N = 16384 case)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--q-quant", default="auto", choices=["auto", "prologue", "pre-pass"],
@@ -139,11 +161,48 @@ def main(argv=None) -> int:
         del src, dst
     R = _load("reference")
     H = _load("hip_impl")
+    head = measure(R, H, args.config, args.steps, args.warmup, args.q_quant)
     case = CONFIGS[args.config]
+    res = {
+        "metric": "sage_attn effective TOPS (4*B*H*N^2*D/t)",
+        "value": head["value"],
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": head["config"],
+        **{key: head[key] for key in ("pct_int8_peak", "algo_tops", "latency_ms", "prepass", "roofline")},
+    }
+    if args.also != "none" and args.also != args.config:
+        # the metric's N = 16384 half: the same measurement on configuration 3
+        other = measure(R, H, args.also, args.steps, args.warmup, args.q_quant)
+        res[f"n{CONFIGS[args.also]['seq_len']}"] = other
+    if not args.no_cpu_baseline:
+        if str(ROOT) not in sys.path:
+            sys.path.insert(0, str(ROOT))
+        res["cpu_baseline"] = cpu_baseline(R, case, args.cpu_budget_s)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
+    """``warmup`` untimed and ``steps`` timed forwards of configuration
+    ``name`` with its inputs resident in HBM: step time (one pair of events
+    around all steps), effective TOPS (the metric) and algorithmic TOPS,
+    p50/p95 of per-step events, the pre-pass's HBM rate, and the attention
+    kernel's roofline from events around its launches on its stream."""
+    case = CONFIGS[name]
     dev = torch.device("cuda:0")
     inp = R.make_inputs(case, "cpu", 0, torch.bfloat16)
     q, k, v = (inp[x].to(dev) for x in ("q", "k", "v"))
-    causal = bool(inp["causal"])
+    del inp
+    causal = bool(case.get("causal", False))
     pv = case.get("pv_dtype", "fp16")
     q_sub = H.q_sub_of(case.get("q_gran", "block"))
     B, Hq, N, D = q.shape
@@ -152,7 +211,7 @@ def main(argv=None) -> int:
 
     out = torch.empty_like(q)
     stream = torch.cuda.current_stream(dev)
-    fused_q = H.fuse_q_default(D) if args.q_quant == "auto" else args.q_quant == "prologue"
+    fused_q = H.fuse_q_default(D) if q_quant == "auto" else q_quant == "prologue"
 
     def step(ev=None):
         if ev is not None:
@@ -167,62 +226,48 @@ def main(argv=None) -> int:
         if ev is not None:
             ev[2].record(stream)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    for i in range(args.steps):
+    for i in range(steps):
         step(evs[i])
     t_end.record(stream)
     torch.cuda.synchronize()
-    total_ms = t_start.elapsed_time(t_end)
-    ms = total_ms / args.steps
+    ms = t_start.elapsed_time(t_end) / steps
     pre_ms = np.array([e[0].elapsed_time(e[1]) for e in evs])
     attn_ms = np.array([e[1].elapsed_time(e[2]) for e in evs])
     step_ms = np.array([e[0].elapsed_time(e[2]) for e in evs])
+    del q, k, v, out
+    torch.cuda.empty_cache()
 
     value = metric_ops / (ms * 1e-3) / 1e12
     # Q (unless the attention kernel quantizes it) and K quantization + V tiles
     pre_bytes = est["prepass_bytes_k" if fused_q else "prepass_bytes"] + est["vtile_bytes"]
+    pre_gbps = pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9
     achieved = algo_ops / (float(attn_ms.mean()) * 1e-3) / 1e12
-    res = {
-        "metric": "sage_attn effective TOPS (4*B*H*N^2*D/t)",
-        "value": round(value, 2),
-        "unit": "TOPS",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "int8",
-        "data": "synthetic",
-        "config": {"workload": f"{args.config}: {case['desc']}", "batch": B, "heads": Hq,
-                   "kv_heads": k.shape[1], "seq_len": N, "head_dim": D, "causal": causal, "pv_dtype": pv,
+    return {
+        "config": {"workload": f"{name}: {case['desc']}", "batch": B, "heads": Hq, "kv_heads": int(case.get(
+                   "num_kv_heads", Hq)), "seq_len": N, "head_dim": D, "causal": causal, "pv_dtype": pv,
                    "q_gran": case.get("q_gran", "block"), "smooth_k": True,
                    "q_quant": "attention prologue" if fused_q else "pre-pass"},
+        "value": round(value, 2),
+        "ms_per_step": round(ms, 4),
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
+        "algo_tops": round(algo_ops / (ms * 1e-3) / 1e12, 2),
         "latency_ms": {"p50": round(float(np.percentile(step_ms, 50)), 4),
                        "p95": round(float(np.percentile(step_ms, 95)), 4)},
-        "prepass": {"ms": round(float(pre_ms.mean()), 4), "bytes": pre_bytes,
-                    "gbps": round(pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9, 1),
-                    "hbm_frac": round(pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)},
+        "prepass": {"ms": round(float(pre_ms.mean()), 4), "bytes": pre_bytes, "gbps": round(pre_gbps, 1),
+                    "hbm_frac": round(pre_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": {"kernel": "attn_fwd_kernel", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": _traffic_from_profiles(args.config),
+                     "traffic": _traffic_from_profiles(name),
                      "launch_ms": round(float(attn_ms.mean()), 4), "algo_ops_per_launch": algo_ops},
     }
-    if not args.no_cpu_baseline:
-        if str(ROOT) not in sys.path:
-            sys.path.insert(0, str(ROOT))
-        res["cpu_baseline"] = cpu_baseline(R, case, args.cpu_budget_s)
-    print(json.dumps(res), flush=True)
-    return 0
 
 
 if __name__ == "__main__":

@@ -83,7 +83,27 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+    build_peak(verbose)
     return LIB
+
+
+PEAK_SRC = PKG / "peak" / "mfma_peak.hip"
+PEAK_EXE = LIBDIR / "mfma_peak"
+
+
+def build_peak(verbose: bool = True) -> Path:
+    """The MFMA-only throughput program (``tribench_amd/lib/mfma_peak``) that
+    measures the dense peaks the roofline figures use."""
+    LIBDIR.mkdir(exist_ok=True)
+    tmp = PEAK_EXE.with_name(PEAK_EXE.name + ".tmp")
+    cmd = [hipcc(), *COMMON, str(PEAK_SRC), "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, PEAK_EXE)
+    if verbose:
+        print(f"built {PEAK_EXE}")
+    return PEAK_EXE
 
 
 def main(argv: list[str] | None = None) -> int:

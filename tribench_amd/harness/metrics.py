@@ -13,10 +13,12 @@ from typing import Any, Callable
 
 # peak rates in T(FL)OPS, and HBM bandwidth in GB/s
 PEAKS_MI355X: dict[str, float] = {
-    "int8": 5033.0,   # 256 CU x 4 SIMD x 2048 ops/clk x 2.4 GHz
-    "fp8": 5033.0,
-    "fp16": 2516.0,
-    "bf16": 2516.0,
+    # the published dense figures (256 CU x 4 SIMD x 2048 or 1024 ops/clk x
+    # 2.4 GHz = 5033 / 2516, rounded as AMD quotes them; bench.py uses the same)
+    "int8": 5000.0,
+    "fp8": 5000.0,
+    "fp16": 2500.0,
+    "bf16": 2500.0,
     "fp32": 157.3,
     "fp64": 78.6,
     "hbm_gbps": 8000.0,
