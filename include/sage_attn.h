@@ -48,7 +48,7 @@
 extern "C" {
 #endif
 
-#define SAGE_ABI_VERSION 5
+#define SAGE_ABI_VERSION 6
 
 /* element types (dtype codes used by every entry point) */
 #define SAGE_DTYPE_F32 0

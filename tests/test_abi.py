@@ -30,6 +30,28 @@ def test_header_declares_the_entry_points():
                                      "sage_vtile_bytes", "sage_vtiles"]
 
 
+def _declared_arg_counts():
+    """Parameter count of every function declared in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(sage_[a-z_0-9]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_bindings_match_the_header_argument_counts(lib):
+    """hip_impl binds every entry point with exactly the header's number of
+    parameters: a signature change on one side without the other fails here
+    instead of passing garbage through ctypes."""
+    counts = _declared_arg_counts()
+    assert set(counts) == set(_declared_functions())
+    for name, n in counts.items():
+        fn = getattr(lib, name)
+        assert fn.argtypes is not None, name
+        assert len(fn.argtypes) == n, f"{name}: header {n} parameters, binding {len(fn.argtypes)}"
+
+
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared_functions():
         assert hasattr(lib, name), name

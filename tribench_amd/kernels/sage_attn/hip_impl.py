@@ -27,7 +27,7 @@ from pathlib import Path
 import numpy as np
 import torch
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 LOG2E_REF = 1.44269504  # triton_impl.py:69
 WAVE_ROWS = 32          # q rows per wavefront of the attention kernel (q_gran="wave")
 # rows per Q scale for each q_gran: one block of 128 rows (the reference), one
@@ -70,6 +70,10 @@ def _load():
     p64 = ctypes.POINTER(ctypes.c_int64)
     lib.sage_abi_version.restype = i32
     lib.sage_abi_version.argtypes = []
+    ver = lib.sage_abi_version()  # before binding the rest: an older library may lack newer symbols
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"sage_attn hip: library ABI {ver}, expected {ABI_VERSION} "
+                           f"({library_path()}; rebuild with `python -m tribench_amd.build`)")
     lib.sage_last_error.restype = ctypes.c_char_p
     lib.sage_last_error.argtypes = []
     lib.sage_prepass_workspace_bytes.restype = sz
@@ -100,9 +104,6 @@ def _load():
     lib.sage_flash_fwd.restype = i32
     lib.sage_flash_fwd.argtypes = [vp, p64, vp, p64, vp, i32, p64, vp, p64, i32, i64, i64, i64, i64, i64, i64, f32,
                                    i32, vp]
-    ver = lib.sage_abi_version()
-    if ver != ABI_VERSION:
-        raise RuntimeError(f"sage_attn hip: library ABI {ver}, expected {ABI_VERSION}")
     _LIB = lib
     return lib
 
