@@ -87,23 +87,27 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     return LIB
 
 
-PEAK_SRC = PKG / "peak" / "mfma_peak.hip"
-PEAK_EXE = LIBDIR / "mfma_peak"
+# Measurement programs (tribench_amd/peak/*.hip -> tribench_amd/lib/<stem>):
+# mfma_peak measures the dense MFMA peaks the roofline figures use,
+# issue_model how a SIMD overlaps the attention loop's instruction mix.
+PEAK_DIR = PKG / "peak"
 
 
-def build_peak(verbose: bool = True) -> Path:
-    """The MFMA-only throughput program (``tribench_amd/lib/mfma_peak``) that
-    measures the dense peaks the roofline figures use."""
+def build_peak(verbose: bool = True) -> list[Path]:
     LIBDIR.mkdir(exist_ok=True)
-    tmp = PEAK_EXE.with_name(PEAK_EXE.name + ".tmp")
-    cmd = [hipcc(), *COMMON, str(PEAK_SRC), "-o", str(tmp)]
-    res = subprocess.run(cmd, capture_output=True, text=True)
-    if res.returncode != 0:
-        raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, PEAK_EXE)
-    if verbose:
-        print(f"built {PEAK_EXE}")
-    return PEAK_EXE
+    exes = []
+    for src in sorted(PEAK_DIR.glob("*.hip")):
+        exe = LIBDIR / src.stem
+        tmp = exe.with_name(exe.name + ".tmp")
+        cmd = [hipcc(), *COMMON, str(src), "-o", str(tmp)]
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
+        os.replace(tmp, exe)
+        exes.append(exe)
+        if verbose:
+            print(f"built {exe}")
+    return exes
 
 
 def main(argv: list[str] | None = None) -> int:
