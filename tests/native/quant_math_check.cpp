@@ -9,6 +9,10 @@
 //                              (t = x/s; t += +-0.5; trunc), and div_rn(x, s,
 //                              RN(1/s)) must equal IEEE x/s for |x| >= 2^-100
 //   divrand <n_scales> <n_x>   random scales in [2^-100, 2^100], random x
+//   fp8div <bf16|f16> <stride> FP8 V codes through Markstein's division against
+//                              IEEE division (div_rn_signed), every 16-bit x
+//                              per stride-th amax
+//   fp8divrand <n_amax> <n_x>  the same for random fp32 amax and x
 //   e4m3 <stride> <out_file>   f32_to_e4m3 of every stride-th bit pattern below
 //                              0x7F800001, written as bytes for comparison with
 //                              the numpy oracle
@@ -94,6 +98,57 @@ int main(int argc, char** argv) {
         const int8_t q = sage::quant_elem(x, s, r, fast), w = ref_quant(x, s);
         if (q != w || (fast && (x >= 0x1p-100f || x <= -0x1p-100f) && sage::div_rn(x, s, r) != x / s)) {
           printf("MISMATCH scale=%a x=%a got %d want %d\n", s, x, q, w);
+          return 1;
+        }
+        ++count;
+      }
+    }
+  } else if (!strcmp(argv[1], "fp8div") && argc == 4) {
+    // FP8 V codes of 16-bit inputs: for every positive finite amax of the
+    // type (every stride-th pattern) with v_scale = amax / 448 in the fast
+    // range and every x of the type with |x| <= amax, both signs, the
+    // kernels' fast path e4m3(div_rn(x, s, RN(1/s))) must equal e4m3(x / s)
+    const bool bf = !strcmp(argv[2], "bf16");
+    const uint32_t stride = (uint32_t)strtoul(argv[3], 0, 10);
+    const uint32_t top = bf ? 0x7F80u : 0x7C00u;  // first non-finite pattern
+    auto value = [bf](uint32_t h) {
+      if (bf) return from_bits(h << 16);
+      const uint32_t e = (h >> 10) & 31u, m = h & 1023u;  // fp16 (finite patterns only)
+      return e ? __builtin_ldexpf((float)(1024u + m), (int)e - 25) : __builtin_ldexpf((float)m, -24);
+    };
+    for (uint32_t ha = 1; ha < top; ha += stride) {
+      const float amax = value(ha);
+      const float s = amax / 448.0f;
+      if (!sage::fast_div_ok(s)) continue;
+      const float r = 1.0f / s;
+      for (uint32_t hx = 0; hx <= ha; ++hx) {
+        for (int sg = 0; sg < 2; ++sg) {
+          const float x = sg ? -value(hx) : value(hx);
+          const uint8_t got = sage::f32_to_e4m3(sage::div_rn_signed(x, s, r)), want = sage::f32_to_e4m3(x / s);
+          if (got != want) {
+            printf("MISMATCH fp8 scale=%a x=%a got %02x want %02x\n", s, x, got, want);
+            return 1;
+          }
+          ++count;
+        }
+      }
+    }
+  } else if (!strcmp(argv[1], "fp8divrand") && argc == 4) {
+    // the same for fp32 inputs: random amax over the fast range, random x
+    const int ns = atoi(argv[2]), nx = atoi(argv[3]);
+    for (int i = 0; i < ns; ++i) {
+      const float amax = from_bits(((uint32_t)(rnd() % 200 + 27) << 23) | (rnd() & 0x7FFFFF));
+      const float s = amax / 448.0f;
+      if (!sage::fast_div_ok(s)) continue;
+      const float r = 1.0f / s;
+      for (int j = 0; j < nx; ++j) {
+        // |x| spread over 2^-24 .. 1 of amax, uniform in the exponent
+        float x = __builtin_ldexpf(amax * (0.5f + 0.5f * (float)(rnd() & 0xFFFFFF) / 16777216.0f), -(int)(rnd() % 25));
+        if (rnd() & 1) x = -x;
+        if (j == 0) x = amax;
+        const uint8_t got = sage::f32_to_e4m3(sage::div_rn_signed(x, s, r)), want = sage::f32_to_e4m3(x / s);
+        if (got != want) {
+          printf("MISMATCH fp8 scale=%a x=%a got %02x want %02x\n", s, x, got, want);
           return 1;
         }
         ++count;

@@ -4,8 +4,10 @@ tests/native/quant_math_check.cpp includes tribench_amd/csrc/sage_quant_math.h
 — the same text the gfx950 kernels compile — and compares it against IEEE
 arithmetic: Markstein's division (sage::div_rn) and the reference rounding
 (triton_impl.py:29-31) exhaustively over the binades where int8 rounding
-happens, plus random scales across the fast-path range; and the FP8 e4m3
-encoder against the numpy oracle (itself pinned to torch.float8_e4m3fn).
+happens, plus random scales across the fast-path range; the FP8 e4m3
+encoder against the numpy oracle (itself pinned to torch.float8_e4m3fn); and
+the FP8 V path's quotient (div_rn_signed, which keeps -0) against IEEE
+division, through the encoder, for every 16-bit input per scale.
 """
 from __future__ import annotations
 
@@ -58,3 +60,14 @@ def test_e4m3_encoder_matches_oracle(checker, tmp_path):
     x = bits.view(np.float32)
     assert np.array_equal(codes[:, 0], O.e4m3_encode(x))
     assert np.array_equal(codes[:, 1], O.e4m3_encode(-x))
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_fp8_division_16bit_inputs(checker, dtype):
+    # every x of the type against every 17th amax (the full sweep, stride 1:
+    # 889,737,154 bf16 and 1,007,713,278 fp16 pairs, passes as well)
+    assert _run(checker, "fp8div", dtype, 17) > 4e7
+
+
+def test_fp8_division_random_fp32(checker):
+    assert _run(checker, "fp8divrand", 2000, 20000) > 3e7

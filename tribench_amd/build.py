@@ -89,17 +89,23 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
 
 # Measurement programs (tribench_amd/peak/*.hip -> tribench_amd/lib/<stem>):
 # mfma_peak measures the dense MFMA peaks the roofline figures use,
-# issue_model how a SIMD overlaps the attention loop's instruction mix.
+# issue_model how a SIMD overlaps the attention loop's instruction mix,
+# hbm_peak what streaming kernels move through HBM.  The device checks of
+# tests/native/*.hip (run by the GPU tests) are built the same way, with the
+# pre-pass's floating-point flags.
 PEAK_DIR = PKG / "peak"
+CHECK_DIR = PKG.parent / "tests" / "native"
 
 
 def build_peak(verbose: bool = True) -> list[Path]:
     LIBDIR.mkdir(exist_ok=True)
     exes = []
-    for src in sorted(PEAK_DIR.glob("*.hip")):
+    srcs = [(s, []) for s in sorted(PEAK_DIR.glob("*.hip"))]
+    srcs += [(s, ["-ffp-contract=off"]) for s in sorted(CHECK_DIR.glob("*.hip"))]
+    for src, extra in srcs:
         exe = LIBDIR / src.stem
         tmp = exe.with_name(exe.name + ".tmp")
-        cmd = [hipcc(), *COMMON, str(src), "-o", str(tmp)]
+        cmd = [hipcc(), *COMMON, *extra, str(src), "-o", str(tmp)]
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")

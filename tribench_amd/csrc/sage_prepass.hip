@@ -4,16 +4,16 @@
 // (kernels/sage_attn/triton_impl.py:7-82) and adds what the reference only
 // hooks (K smoothing, triton_impl.py:39-40) or lacks (per-channel FP8 V).
 //
-// Two launches:
-//   A  (one grid, roles by block index)
-//        K statistics:  per (chunk, kv-head, batch) fp32 channel sums of K
-//                       (and channel max|v| for FP8 V) in a fixed order
-//        Q quant:       per (128-row block, head, batch) INT8 + scale(s)
-//        K quant:       here as well when no K statistics are needed
-//   B  K quant with the channel mean subtracted (+ FP8 V quant)
-// and, through sage_prepass_vt, the V tiles of sage_vtiles: in launch A with
-// fp16/bf16 P.V (they need nothing from the statistics), in launch B with
-// FP8 P.V (their codes need v_scale).
+// Roles (one 256-thread block each, chosen by block index):
+//   K statistics:  per (chunk, kv-head, batch) fp32 channel sums of K (and
+//                  channel max|v| for FP8 V) in a fixed order
+//   Q quant:       per (128-row block, head, batch) INT8 + scale(s)
+//   K quant:       with the channel mean subtracted (+ FP8 V rows)
+//   V tiles:       through sage_prepass_vt, the tiles of sage_vtiles (FP8
+//                  tiles need v_scale, fp16/bf16 ones nothing)
+// With statistics (K smoothing, FP8 V) launch A runs them and every role
+// independent of them; launch B the K quant and the FP8 V tiles, which need
+// the head's channel means and scales.  Without statistics launch A alone.
 //
 // Every block is 256 threads.  A block's data is read once from HBM with
 // 16-byte loads, held in registers while the block's max|x| is reduced, then
@@ -89,8 +89,8 @@ constexpr int vtile_pool_bytes() {
 // One quantization block: rows [0, rows_valid) of blk rows x D, scale per
 // q_sub rows (q_sub == blk: one scale per block, triton_impl.py:28,33;
 // q_sub == 1: one scale per row).
-// x = fp32(in) * mul (if use_mul) - km[c] (if km); tail rows are left out of
-// the block max and not stored.  NI = 16-element items per thread
+// x = fp32(in) * mul (if use_mul) - km[c] (if km_s; km[c] at stat_slot(c));
+// tail rows are left out of the block max and not stored.  NI = 16-element items per thread
 // (blk * D / 4096, at least 1; with fewer items than threads whole waves idle).
 // ---------------------------------------------------------------------------
 struct NoHook {
@@ -129,11 +129,12 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
   }
   after_loads();
   // the thread's 16 channels are the same in every item (256 % CPR == 0):
-  // their means go to registers once, not through LDS for every element
+  // their means go to registers once, not through LDS for every element.
+  // Without smoothing they are +0, and x - (+0) == x for every x (-0 too).
   static_assert(kPrepassThreads % CPR == 0, "items of a thread share their channels");
   float kmr[16];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) kmr[e] = km_s ? km_s[(tid % CPR) * 16 + e] : 0.0f;
+  for (int e = 0; e < 16; ++e) kmr[e] = km_s ? km_s[stat_slot((tid % CPR) * 16 + e)] : 0.0f;
 #pragma unroll
   for (int j = 0; j < NI; ++j) {
     const int it = tid + kPrepassThreads * j;
@@ -144,7 +145,7 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
       for (int e = 0; e < 16; ++e) {
         float x = elem<T>(raw[j][e >> 3], e & 7);
         if (use_mul) x = x * mul;
-        if (km_s) x = x - kmr[e];
+        x = x - kmr[e];
         am = fmaxf(am, fabsf(x));
       }
     }
@@ -175,7 +176,7 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
         for (int e = 0; e < 16; ++e) {
           float x = elem<T>(raw[j][e >> 3], e & 7);
           if (use_mul) x = x * mul;
-          if (km_s) x = x - kmr[e];
+          x = x - kmr[e];
           const int8_t qv = quant_elem(x, sc[j], rc[j], kFast);
           w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
         }
@@ -230,7 +231,7 @@ __device__ __forceinline__ void quant_block(const T* __restrict__ src, int64_t s
       for (int e = 0; e < 16; ++e) {
         float x = elem<T>(raw[j][e >> 3], e & 7);
         if (use_mul) x = x * mul;
-        if (km_s) x = x - kmr[e];
+        x = x - kmr[e];
         const int8_t qv = quant_elem(x, sc, rc, kFast);
         w[e >> 2] |= ((uint32_t)(uint8_t)qv) << (8 * (e & 3));
       }
@@ -288,66 +289,97 @@ __device__ __forceinline__ void kstats_chunk(const T* __restrict__ ksrc, int64_t
       }
     }
   }
-  // tree over the TL token lanes: acc[tl] += acc[tl + s], s = TL/2 .. 1
-  float* row = red_s + tl * D + cg * 8;
+  // tree over the TL token lanes: acc[tl] += acc[tl + s], s = TL/2 .. 1.
+  // Row r of red_s holds channel group cg's values 0-3 and 4-7 as 16-byte
+  // units cg and CG + cg, swapped in odd rows, so that the units a wave
+  // writes or reads together never share a bank.
+  auto at = [&](int r, int e) { return red_s + r * D + 4 * (cg + CG * ((e >> 2) ^ (r & 1))) + (e & 3); };
 #pragma unroll
-  for (int e = 0; e < 8; ++e) row[e] = acc[e];
+  for (int e = 0; e < 8; ++e) *at(tl, e) = acc[e];
   __syncthreads();
   for (int s = TL / 2; s >= 1; s >>= 1) {
     if (tl < s) {
-      const float* o = red_s + (tl + s) * D + cg * 8;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) row[e] = row[e] + o[e];
+      for (int e = 0; e < 8; ++e) *at(tl, e) = *at(tl, e) + *at(tl + s, e);
     }
     __syncthreads();
   }
   if (psum && tl == 0) {  // (no K smoothing: FP8 V statistics only, no sums)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) psum[cg * 8 + e] = row[e];
+    for (int e = 0; e < 8; ++e) psum[cg * 8 + e] = *at(0, e);
   }
   if (vsrc) {
     __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 8; ++e) row[e] = vm[e];
+    for (int e = 0; e < 8; ++e) *at(tl, e) = vm[e];
     __syncthreads();
     for (int s = TL / 2; s >= 1; s >>= 1) {
       if (tl < s) {
-        const float* o = red_s + (tl + s) * D + cg * 8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) row[e] = fmaxf(row[e], o[e]);
+        for (int e = 0; e < 8; ++e) *at(tl, e) = fmaxf(*at(tl, e), *at(tl + s, e));
       }
       __syncthreads();
     }
     if (tl == 0) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pamax[cg * 8 + e] = row[e];
+      for (int e = 0; e < 8; ++e) pamax[cg * 8 + e] = *at(0, e);
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// FP8 e4m3 V block: v8 = RNE_sat(v / v_scale[c]) (v_scale[c] == 0 -> 0)
+// FP8 e4m3 V rows [0, rows_valid) of one block: v8 = RNE_sat(v / v_scale[c])
+// (v_scale[c] == 0 -> 0).  A thread's items keep its 16 channels (256 % CPR
+// == 0), so their scales and reciprocals sit in registers; the quotient is
+// Markstein's (div_rn_signed) and the codes the packed conversion when every
+// scale of the wave lies in the fast range, IEEE division and f32_to_e4m3
+// otherwise.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__device__ __forceinline__ void vquant_block(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
-                             const float* vs_s, uint8_t* __restrict__ dst, int64_t dn) {
+__device__ __forceinline__ void vquant_rows(const T* __restrict__ src, int64_t sn, int rows_valid, int blk,
+                                            const float* vs_s, uint8_t* __restrict__ dst, int64_t dn) {
   constexpr int CPR = D / 16;
-  const int nit = blk * CPR;
-  for (int it = threadIdx.x; it < nit; it += kPrepassThreads) {
-    const int row = it / CPR, c = it % CPR;
-    if (row >= rows_valid) continue;
-    const T* p = src + (int64_t)row * sn + c * 16;
-    Raw8<T> r0 = load8<T>(p), r1 = load8<T>(p + 8);
-    uint32_t w[4] = {0u, 0u, 0u, 0u};
+  const int t = (int)threadIdx.x;
+  const int c = t % CPR;
+  float sc[16], rc[16];
+  bool ok = true;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float x = elem<T>(e < 8 ? r0 : r1, e & 7);
-      const float s = vs_s[c * 16 + e];
-      const float t = s > 0.0f ? x / s : 0.0f;
-      w[e >> 2] |= ((uint32_t)f32_to_e4m3(t)) << (8 * (e & 3));
-    }
-    *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  for (int e = 0; e < 16; ++e) {
+    sc[e] = vs_s[stat_slot(c * 16 + e)];
+    rc[e] = sc[e] > 0.0f ? 1.0f / sc[e] : 0.0f;
+    ok = ok && fast_div_ok(sc[e]);
   }
+  auto rows = [&](auto fast_tag) __attribute__((always_inline)) {
+    constexpr bool kFast = decltype(fast_tag)::value;
+    for (int it = t; it < blk * CPR; it += kPrepassThreads) {
+      const int row = it / CPR;
+      if (row >= rows_valid) continue;
+      const T* p = src + (int64_t)row * sn + c * 16;
+      const Raw8<T> r0 = load8<T>(p), r1 = load8<T>(p + 8);
+      uint32_t w[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = elem<T>(g < 2 ? r0 : r1, (4 * g + i) & 7);
+        if constexpr (kFast) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = div_rn_signed(x[i], sc[4 * g + i], rc[4 * g + i]);
+          w[g] = e4m3x4(x[0], x[1], x[2], x[3]);
+        } else {
+          w[g] = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float s = sc[4 * g + i];
+            w[g] |= (uint32_t)f32_to_e4m3(s > 0.0f ? x[i] / s : 0.0f) << (8 * i);
+          }
+        }
+      }
+      *reinterpret_cast<uint4*>(dst + (int64_t)row * dn + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  };
+  if (__builtin_amdgcn_ballot_w64(!ok) == 0) rows(std::true_type{});
+  else rows(std::false_type{});
 }
 
 template <typename T, int D, int NI>
@@ -431,7 +463,7 @@ __device__ __forceinline__ void head_stats(const PrepassArgs& a, int64_t b, int6
     for (int c = 1; c < 16; ++c)
       if (c < a.nch) s = s + part[c];
     const float m = s / (float)a.Nkv;
-    km_s[tid] = m;
+    km_s[stat_slot(tid)] = m;
     if (write_out) a.km[(b * a.Hkv + h) * D + tid] = m;
   }
   if (a.v_fp8 && vs_s) {
@@ -440,7 +472,7 @@ __device__ __forceinline__ void head_stats(const PrepassArgs& a, int64_t b, int6
     for (int c = 1; c < 16; ++c)
       if (c < a.nch) m = fmaxf(m, a.pamax[base + c * D + tid]);
     const float sc = m / 448.0f;
-    vs_s[tid] = sc;
+    vs_s[stat_slot(tid)] = sc;
     if (write_out) a.v_scale[(b * a.Hkv + h) * D + tid] = sc;
   }
 }
@@ -450,7 +482,7 @@ template <typename T, int D, int NIQ, int NIK>
 __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs a) {
   __shared__ uint32_t amax_s[16];
   __shared__ float scl_s[16], rcp_s[16];
-  __shared__ float km_s[D], vs_s[D];
+  __shared__ float km_s[stat_lds_floats<D>()], vs_s[stat_lds_floats<D>()];
   __shared__ __attribute__((aligned(16))) char pool[vtile_pool_bytes<D>()];
   int64_t r = blockIdx.x;
   if (r >= a.n_kblk_b + a.n_qblk_b) {
@@ -477,7 +509,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_b_kernel(PrepassArgs 
     const int rows_valid = (int)min<int64_t>(a.blkk, a.Nkv - row0);
     const T* src = static_cast<const T*>(a.v) + b * a.sv[0] + h * a.sv[1] + row0 * a.sv[2];
     uint8_t* dst = a.v8 + b * a.sv8[0] + h * a.sv8[1] + row0 * a.sv8[2];
-    vquant_block<T, D>(src, a.sv[2], rows_valid, a.blkk, vs_s, dst, a.sv8[2]);
+    vquant_rows<T, D>(src, a.sv[2], rows_valid, a.blkk, vs_s, dst, a.sv8[2]);
   }
 }
 

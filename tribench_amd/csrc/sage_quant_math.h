@@ -35,6 +35,14 @@ SAGE_HD inline float div_rn(float x, float scale, float rcp) {
   return __builtin_fmaf(e, rcp, q0);
 }
 
+// div_rn with the sign of a zero quotient kept: x = -0 gives -0, as IEEE
+// division does (div_rn's residual is +0 there, which turns the sum into
+// +0).  Needed where the quotient's sign survives the rounding (FP8 codes:
+// -0 encodes as 0x80); for nonzero x the sign is already that of x.
+SAGE_HD inline float div_rn_signed(float x, float scale, float rcp) {
+  return __builtin_copysignf(div_rn(x, scale, rcp), x);
+}
+
 // The reference's rounding (triton_impl.py:29-31): t += 0.5*sign(t) in fp32,
 // then truncate toward zero.  Note fp32(0.49999997 + 0.5) == 1.0.
 SAGE_HD inline int round_half_away(float t) {

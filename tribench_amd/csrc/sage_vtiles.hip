@@ -26,11 +26,11 @@ struct VtileArgs {
 template <typename T, int D, int PVM>
 __global__ __launch_bounds__(256) void vtile_kernel(VtileArgs a) {
   __shared__ __attribute__((aligned(16))) char tile_s[vtile_lds_bytes<D, PVM>()];
-  __shared__ float vs_s[D];
+  __shared__ float vs_s[stat_lds_floats<D>()];
   const int64_t r = blockIdx.x;
   const int64_t t = r % a.ntile, h = (r / a.ntile) % a.Hkv, b = r / (a.ntile * a.Hkv);
   if constexpr (PVM == SAGE_PV_FP8) {
-    if (threadIdx.x < D) vs_s[threadIdx.x] = a.v_scale[(b * a.Hkv + h) * D + threadIdx.x];
+    if (threadIdx.x < D) vs_s[stat_slot(threadIdx.x)] = a.v_scale[(b * a.Hkv + h) * D + threadIdx.x];
     __syncthreads();
   }
   constexpr int EB = PVM == SAGE_PV_FP8 ? 1 : 2;
