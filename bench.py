@@ -15,7 +15,11 @@ SDPA (a restatement of reference.py:ref) on a bounded sample of the same
 workload on this host's cores.  The metric is quoted at N = 4096 and 16384:
 after the headline configuration the same run times configuration 3 (B=2,
 H=32, N=16384, causal) and reports it as the nested ``n16384`` object, with
-its own step time, effective and algorithmic TOPS and roofline.
+its own step time, effective and algorithmic TOPS and roofline.  ``prepass``
+gives the pre-pass's algorithmic bytes per second (K and V read once, K8 and
+the V tiles written once; Q too where the pre-pass quantizes it) as a
+fraction of the published 8 TB/s (``hbm_frac``) and of a plain 1 GiB device
+copy timed on the same box first (``copy_gbps``, ``frac_of_copy``).
 
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2] [--also cfg3|none]
                   [--no-cpu-baseline] [--copy-probe-gib G] [--q-quant auto|prologue|pre-pass]
@@ -159,9 +163,11 @@ def main(argv=None) -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    copy_gbps = copy_rate_gbps()
     R = _load("reference")
     H = _load("hip_impl")
     head = measure(R, H, args.config, args.steps, args.warmup, args.q_quant)
+    _with_copy_rate(head, copy_gbps)
     case = CONFIGS[args.config]
     res = {
         "metric": "sage_attn effective TOPS (4*B*H*N^2*D/t)",
@@ -182,6 +188,7 @@ def main(argv=None) -> int:
     if args.also != "none" and args.also != args.config:
         # the metric's N = 16384 half: the same measurement on configuration 3
         other = measure(R, H, args.also, args.steps, args.warmup, args.q_quant)
+        _with_copy_rate(other, copy_gbps)
         res[f"n{CONFIGS[args.also]['seq_len']}"] = other
     if not args.no_cpu_baseline:
         if str(ROOT) not in sys.path:
@@ -189,6 +196,33 @@ def main(argv=None) -> int:
         res["cpu_baseline"] = cpu_baseline(R, case, args.cpu_budget_s)
     print(json.dumps(res), flush=True)
     return 0
+
+
+def copy_rate_gbps(gib: int = 1, reps: int = 5) -> float:
+    """What a plain device-to-device copy moves on this box (read + written
+    bytes per second, median of ``reps`` copies of ``gib`` GiB): the practical
+    scale for the pre-pass's rate beside the published 8 TB/s."""
+    n = gib << 30
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2.0 * n / (float(np.median(times)) * 1e-3) / 1e9
+
+
+def _with_copy_rate(res: dict, copy_gbps: float) -> None:
+    pre = res["prepass"]
+    pre["copy_gbps"] = round(copy_gbps, 1)
+    pre["frac_of_copy"] = round(pre["gbps"] / copy_gbps, 4)
 
 
 def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
