@@ -11,9 +11,10 @@
 //   K quant:       with the channel mean subtracted (+ FP8 V rows)
 //   V tiles:       through sage_prepass_vt, the tiles of sage_vtiles (FP8
 //                  tiles need v_scale, fp16/bf16 ones nothing)
-// With statistics (K smoothing, FP8 V) launch A runs them and every role
-// independent of them; launch B the K quant and the FP8 V tiles, which need
-// the head's channel means and scales.  Without statistics launch A alone.
+// With statistics (K smoothing, FP8 V) launch A runs them; launch B the K
+// quant, which needs the head's channel means, the Q quant and the V tiles
+// (the fp16/bf16 ones in launch A when launch B has Q blocks).  Without
+// statistics launch A alone.
 //
 // Every block is 256 threads.  A block's data is read once from HBM with
 // 16-byte loads, held in registers while the block's max|x| is reduced, then
@@ -660,12 +661,15 @@ static int prepass_impl(const char* who, const void* q, const void* k, const voi
   a.n_kblk_a = need_b ? 0 : a.nkb * Hkv * B;
   a.n_kblk_b = need_b ? a.nkb * Hkv * B : 0;
   a.n_qblk_b = need_b && do_q ? a.nqb * Hq * B : 0;
-  // V tiles last in their launch: A for fp16/bf16, B for FP8 (v_scale)
+  // V tiles last in their launch: B for FP8 (they need v_scale), and B for
+  // fp16/bf16 too when B quantizes only K (its VALU-bound K blocks then share
+  // the launch with copy-like work, and launch A only reads K); A otherwise
   a.vt = static_cast<uint8_t*>(vt);
   a.pv_mode = pv_mode;
   a.ntile = (Nkv + 63) / 64;
-  a.n_vt_a = vt && pv_mode != SAGE_PV_FP8 ? a.ntile * Hkv * B : 0;
-  a.n_vt_b = vt && pv_mode == SAGE_PV_FP8 ? a.ntile * Hkv * B : 0;
+  const bool vt_in_b = vt && (pv_mode == SAGE_PV_FP8 || (need_b && !do_q));
+  a.n_vt_a = vt && !vt_in_b ? a.ntile * Hkv * B : 0;
+  a.n_vt_b = vt_in_b ? a.ntile * Hkv * B : 0;
   if (a.n_stat + a.n_qblk_a + a.n_kblk_a + a.n_vt_a > 0x7FFFFFFF || a.n_kblk_b + a.n_qblk_b + a.n_vt_b > 0x7FFFFFFF)
     return fail("%s: invalid argument: grid too large", who);
 
