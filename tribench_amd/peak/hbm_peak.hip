@@ -10,9 +10,10 @@
 //   read2write1 2 bytes read per byte written (a 16-bit to 8-bit conversion,
 //               the mix of quantizing K)
 // each with ordinary and with nontemporal stores, and each at several grid
-// sizes (work-groups of 256 threads per CU).  One JSON line per mix: the
-// best rate over the grid sizes (median of 5 timed launches after a warm-up,
-// hipEvents) and the grid size that gave it.
+// sizes (work-groups of 256 threads per CU) and 4 or 8 16-byte accesses in
+// flight per thread.  One JSON line per mix: the best rate over those shapes
+// (median of 5 timed launches after a warm-up, hipEvents) and the shape that
+// gave it.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -32,8 +33,6 @@
 enum Mix { kRead = 0, kWrite = 1, kCopy = 2, kR2W1 = 3 };
 static const char* kMixName[] = {"read", "write", "copy", "read2write1"};
 
-constexpr int kUnroll = 4;
-
 template <int M, bool NT>
 __device__ __forceinline__ void put(uint4* p, uint4 v) {
   if constexpr (NT) {
@@ -48,7 +47,7 @@ __device__ __forceinline__ void put(uint4* p, uint4 v) {
 
 // n: 16-byte destination items (kRead: source items).  kR2W1 reads src[2i]
 // and src[2i+1] for destination item i, so src holds 2n items there.
-template <int M, bool NT>
+template <int M, bool NT, int kUnroll>
 __global__ __launch_bounds__(256) void stream_kernel(const uint4* __restrict__ src, uint4* __restrict__ dst,
                                                      int64_t n, uint32_t* sink) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -90,30 +89,36 @@ static void run(const uint4* src, uint4* dst, uint32_t* sink, int64_t bytes, int
   CHECK(hipEventCreate(&e0));
   CHECK(hipEventCreate(&e1));
   double best = 0.0;
-  int best_wg = 0;
-  for (int wg : {2, 4, 8, 16, 32}) {
-    const dim3 grid((unsigned)(cus * wg));
-    hipLaunchKernelGGL((stream_kernel<M, NT>), grid, dim3(256), 0, 0, src, dst, n, sink);
-    CHECK(hipGetLastError());
-    std::vector<float> ms(5);
-    for (float& t : ms) {
-      CHECK(hipEventRecord(e0, 0));
-      hipLaunchKernelGGL((stream_kernel<M, NT>), grid, dim3(256), 0, 0, src, dst, n, sink);
-      CHECK(hipGetLastError());
-      CHECK(hipEventRecord(e1, 0));
-      CHECK(hipEventSynchronize(e1));
-      CHECK(hipEventElapsedTime(&t, e0, e1));
-    }
-    std::sort(ms.begin(), ms.end());
-    const double tbs = moved / (ms[2] * 1e-3) / 1e12;
-    if (tbs > best) {
-      best = tbs;
-      best_wg = wg;
+  int best_wg = 0, best_u = 0;
+  for (int u : {4, 8}) {
+    for (int wg : {1, 2, 4, 8, 16, 32}) {
+      const dim3 grid((unsigned)(cus * wg));
+      auto launch = [&]() {
+        if (u == 4) hipLaunchKernelGGL((stream_kernel<M, NT, 4>), grid, dim3(256), 0, 0, src, dst, n, sink);
+        else hipLaunchKernelGGL((stream_kernel<M, NT, 8>), grid, dim3(256), 0, 0, src, dst, n, sink);
+        CHECK(hipGetLastError());
+      };
+      launch();
+      std::vector<float> ms(5);
+      for (float& t : ms) {
+        CHECK(hipEventRecord(e0, 0));
+        launch();
+        CHECK(hipEventRecord(e1, 0));
+        CHECK(hipEventSynchronize(e1));
+        CHECK(hipEventElapsedTime(&t, e0, e1));
+      }
+      std::sort(ms.begin(), ms.end());
+      const double tbs = moved / (ms[2] * 1e-3) / 1e12;
+      if (tbs > best) {
+        best = tbs;
+        best_wg = wg;
+        best_u = u;
+      }
     }
   }
   std::printf("{\"mix\": \"%s\", \"nontemporal_stores\": %s, \"bytes_moved\": %.0f, \"tb_per_s\": %.3f, "
-              "\"frac_of_8tbs\": %.3f, \"workgroups_per_cu\": %d}\n",
-              kMixName[M], NT ? "true" : "false", moved, best, best / 8.0, best_wg);
+              "\"frac_of_8tbs\": %.3f, \"workgroups_per_cu\": %d, \"accesses_in_flight_per_thread\": %d}\n",
+              kMixName[M], NT ? "true" : "false", moved, best, best / 8.0, best_wg, best_u);
   std::fflush(stdout);
   CHECK(hipEventDestroy(e0));
   CHECK(hipEventDestroy(e1));
