@@ -202,35 +202,42 @@ def test_vtiles_nhd_matches_hnd(pack_ref, hip_impl, gpu_device):
 # The pre-pass with the V tiles in its own launches (sage_prepass_vt, what
 # run() uses): every output equals the separate calls' (and so the oracle's,
 # which the tests above pin), the tiles byte for byte, for each placement of
-# the tile role: launch A beside the statistics (fp16/bf16), the single
-# launch without statistics, launch B beside the K quantization (FP8).
-# (B, Hq, Hkv, N, D, dtype, pv, smooth_k, q_sub, layout)
+# the tile role: launch A beside the statistics (fp16/bf16 with Q quantized in
+# the pre-pass), launch B beside the K quantization (FP8, and fp16/bf16 when
+# Q is left to the attention prologue: quant_q False), the single launch
+# without statistics.
+# (B, Hq, Hkv, N, D, dtype, pv, smooth_k, q_sub, layout, quant_q)
 VT_CASES = [
-    (1, 2, 2, 256, 64, "fp32", "fp16", True, 128, "HND"),
-    (2, 4, 2, 300, 128, "bf16", "fp16", True, 128, "HND"),
-    (2, 4, 2, 300, 128, "bf16", "bf16", False, 128, "HND"),
-    (1, 3, 3, 1000, 64, "fp16", "fp8", True, 32, "HND"),
-    (1, 6, 1, 777, 128, "bf16", "fp8", False, 1, "NHD"),
-    (1, 4, 4, 4096, 128, "bf16", "fp16", True, 128, "HND"),
+    (1, 2, 2, 256, 64, "fp32", "fp16", True, 128, "HND", True),
+    (2, 4, 2, 300, 128, "bf16", "fp16", True, 128, "HND", True),
+    (2, 4, 2, 300, 128, "bf16", "bf16", False, 128, "HND", True),
+    (1, 3, 3, 1000, 64, "fp16", "fp8", True, 32, "HND", True),
+    (1, 6, 1, 777, 128, "bf16", "fp8", False, 1, "NHD", True),
+    (1, 4, 4, 4096, 128, "bf16", "fp16", True, 128, "HND", True),
+    (2, 4, 2, 300, 128, "bf16", "fp16", True, 128, "HND", False),
+    (1, 4, 4, 4096, 128, "bf16", "bf16", True, 128, "HND", False),
+    (1, 2, 2, 257, 64, "fp32", "fp16", True, 128, "NHD", False),
+    (1, 2, 1, 1000, 128, "fp16", "fp16", False, 128, "HND", False),
 ]
 
 
 @pytest.mark.parametrize("case", VT_CASES, ids=lambda c: f"B{c[0]}Hq{c[1]}Hkv{c[2]}N{c[3]}D{c[4]}-{c[5]}-{c[6]}"
-                         f"-smooth{int(c[7])}-qsub{c[8]}-{c[9]}")
+                         f"-smooth{int(c[7])}-qsub{c[8]}-{c[9]}-q{int(c[10])}")
 def test_prepass_vt_equals_separate_calls(case, pack_ref, hip_impl, gpu_device):
-    B, Hq, Hkv, N, D, dtype, pv, smooth, q_sub, layout = case
+    B, Hq, Hkv, N, D, dtype, pv, smooth, q_sub, layout, quant_q = case
     print(f"[prepass-vt] {case}", flush=True)
     inp = _inputs(pack_ref, B, Hq, Hkv, N, D, dtype, 2.0, "student_t" if pv == "fp8" else "normal")
     q, k, v = (inp[x].to(gpu_device) for x in ("q", "k", "v"))
     if layout == "NHD":
         q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
     kw = dict(q_sub=q_sub, smooth_k=smooth, tensor_layout=layout)
-    fused = hip_impl.prepass(q, k, v, pv_dtype=pv, **kw)
+    fused = hip_impl.prepass(q, k, v, pv_dtype=pv, quant_q=quant_q, **kw)
     plain = hip_impl.prepass(q, k, v, v_fp8=pv == "fp8", **kw)
     tiles = hip_impl.vtiles(v, pv, plain.get("v_scale"), tensor_layout=layout)
     torch.cuda.synchronize()
     assert torch.equal(fused["vt"], tiles)
-    for key in ("q8", "q_scale", "k8", "k_scale") + (("km",) if smooth else ()) + (("v_scale",) if pv == "fp8" else ()):
+    keys = (("q8", "q_scale") if quant_q else ()) + ("k8", "k_scale")
+    for key in keys + (("km",) if smooth else ()) + (("v_scale",) if pv == "fp8" else ()):
         assert torch.equal(fused[key], plain[key]), key
 
 
