@@ -653,8 +653,8 @@ static int prepass_impl(const char* who, const void* q, const void* k, const voi
   a.nqb = (Nq + blkq - 1) / blkq;
   a.nkb = (Nkv + blkk - 1) / blkk;
   const bool need_b = a.smooth_k || a.v_fp8;
-  // Launch A computes the K statistics; launch B then quantizes K (re-read
-  // while it is likely still in the Infinity Cache) and Q.  Without
+  // Launch A computes the K statistics; launch B then quantizes K (read
+  // again: the statistics of a head must be complete first) and Q.  Without
   // statistics everything runs in launch A.
   a.n_stat = need_b ? a.nch * Hkv * B : 0;
   a.n_qblk_a = need_b || !do_q ? 0 : a.nqb * Hq * B;
