@@ -22,6 +22,9 @@
 //   ds_read_b64    24 reads of 8 bytes per lane
 //   pipeline       one iteration of the attention loop's data flow without
 //                  global memory (as issue_model.hip's pipeline test)
+//   pipeline64     the same data flow with 64 query rows per wave and one
+//                  wave per SIMD (4-wave work-groups; issue_model.hip's
+//                  pipeline64): half the LDS operand bytes per block
 // Output: one JSON line per test (cycles per step, clock, board watts,
 // instructions of the class per second on the device).
 //
@@ -61,7 +64,8 @@ typedef float f2 __attribute__((ext_vector_type(2)));
   } while (0)
 
 constexpr int kLds = 120 * 1024;
-enum Test { kIdle, kMfmaI8, kMfmaF16, kMfmaI8s, kMfmaF16s, kMfmaF8, kFma, kExp, kPkAdd, kLds128, kLds64, kPipeline };
+enum Test { kIdle, kMfmaI8, kMfmaF16, kMfmaI8s, kMfmaF16s, kMfmaF8, kFma, kExp, kPkAdd, kLds128, kLds64, kPipeline,
+            kPipeline64 };
 static const char* kName[] = {"idle(s_sleep)",
                               "mfma_i32_32x32x32_i8",
                               "mfma_f32_32x32x16_f16",
@@ -73,11 +77,13 @@ static const char* kName[] = {"idle(s_sleep)",
                               "v_pk_add_f16",
                               "ds_read_b128",
                               "ds_read_b64",
-                              "pipeline(attention iteration)"};
+                              "pipeline(attention iteration)",
+                              "pipeline64(64 rows per wave, 1 wave per SIMD)"};
 // instructions of the measured class per wave and step
-static const int kPerStep[] = {0, 8, 8, 8, 8, 8, 16, 16, 16, 24, 24, 24};
+static const int kPerStep[] = {0, 8, 8, 8, 8, 8, 16, 16, 16, 24, 24, 24, 48};
 // steps per launch: 5-15 ms each
-static const int kStepsPerLaunch[] = {20000, 60000, 60000, 60000, 60000, 30000, 60000, 60000, 60000, 25000, 25000, 8000};
+static const int kStepsPerLaunch[] = {20000, 60000, 60000, 60000, 60000, 30000, 60000, 60000, 60000, 25000, 25000, 8000,
+                                      4000};
 
 template <int T>
 __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int steps, float seed) {
@@ -259,6 +265,113 @@ __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int st
   }
 }
 
+// 64 query rows per wave, one wave per SIMD (4 waves per work-group): the
+// wave's halves h = 0, 1 of 32 rows, half 0 one block ahead.  Phase X: P.V of
+// half 0 (block i) and QK of half 1 (block i+1) while the VALU forms half 1's
+// P (block i); phase Y: P.V of half 1 and QK of half 0 (block i+2) while it
+// forms half 0's P (block i+1).  Each LDS operand read feeds two MFMAs.
+// A step is one block of 64 keys for the wave's 64 rows.
+__global__ __launch_bounds__(256) void probe64(long long* out, float* sink, int steps, float seed) {
+  __shared__ __attribute__((aligned(16))) char lds[kLds];
+  const int tid = threadIdx.x, lane = tid & 63;
+  for (int i = tid; i < kLds / 4; i += blockDim.x)
+    reinterpret_cast<uint32_t*>(lds)[i] = ((i * 2654435761u) ^ 0x5bd1e995u) & 0xBBFFBBFFu;
+  __syncthreads();
+  v16f o0[4] = {}, o1[4] = {};
+  v4i q0[4], q1[4];
+  for (int k = 0; k < 4; ++k)
+    for (int e = 0; e < 4; ++e) {
+      q0[k][e] = (int)((uint32_t)(lane * 131 + k * 17 + e * 7 + 1) * 2654435761u);
+      q1[k][e] = (int)((uint32_t)(lane * 137 + k * 19 + e * 5 + 3) * 2654435761u);
+    }
+  const int magic = 0x4B400000;
+  v16i S0a[2], S0b[2], S1a[2], S1b[2];
+  uint32_t P0[16], P1[16];
+  for (int t = 0; t < 2; ++t)
+    for (int v = 0; v < 16; ++v) {
+      S0a[t][v] = magic + v * 37 + lane;
+      S0b[t][v] = magic - v * 41 - lane;
+      S1a[t][v] = magic + v * 43 + 2 * lane;
+      S1b[t][v] = magic - v * 47 - 2 * lane;
+    }
+  for (int w = 0; w < 16; ++w) {
+    P0[w] = 0x3C003C00u ^ (uint32_t)(lane * w);
+    P1[w] = 0x3C003C01u ^ (uint32_t)(lane + w);
+  }
+  float l0 = 0.0f, l1 = 0.0f;
+  const float csc = 1e-4f * seed, bias = 12582912.0f * csc;
+  const int koff = lane * 16, voff = 8192 + lane * 16;
+  const v16i mg = {magic, magic, magic, magic, magic, magic, magic, magic,
+                   magic, magic, magic, magic, magic, magic, magic, magic};
+  // 16 P.V MFMAs into o with P pv, 8 QK MFMAs of q into sq, the softmax of ss
+  auto phase = [&](v16f (&o)[4], const uint32_t (&pv)[16], const v4i (&q)[4], v16i (&sq)[2], const v16i (&ss)[2],
+                   uint32_t (&pout)[16], float& lsum, int kofs, int vofs) __attribute__((always_inline)) {
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const v4i va = *reinterpret_cast<const v4i*>(lds + vofs + voff + 1024 * (4 * dt + kk));
+        const v4i pb = {(int)pv[4 * kk], (int)pv[4 * kk + 1], (int)pv[4 * kk + 2], (int)pv[4 * kk + 3]};
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, va), __builtin_bit_cast(v8h, pb),
+                                                       o[dt], 0, 0, 0);
+      }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const v4i ka = *reinterpret_cast<const v4i*>(lds + kofs + koff + 1024 * (4 * t + k));
+        sq[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(ka, q[k], k == 0 ? mg : sq[t], 0, 0, 0);
+      }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float p[16];
+#pragma unroll
+      for (int v = 0; v < 16; ++v) p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(ss[t][v]), csc, -bias));
+#pragma unroll
+      for (int w = 0; w < 8; ++w)
+        pout[8 * t + w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){p[2 * w], p[2 * w + 1]}, h2));
+    }
+    h2 hs[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) hs[w] = __builtin_bit_cast(h2, pout[w]) + __builtin_bit_cast(h2, pout[8 + w]);
+#pragma unroll
+    for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+      for (int i = 0; i < w; ++i) hs[i] = hs[i] + hs[i + w];
+    lsum = __builtin_amdgcn_fdot2(hs[0], (h2){(_Float16)1.0f, (_Float16)1.0f}, lsum, false);
+  };
+  auto iter = [&](v16i (&S0c)[2], v16i (&S0n)[2], v16i (&S1c)[2], v16i (&S1n)[2], int it)
+                  __attribute__((always_inline)) {
+    const int s0 = (it % 3) * 24576, s1 = ((it + 1) % 3) * 24576, s2 = ((it + 2) % 3) * 24576;
+    phase(o0, P0, q1, S1n, S1c, P1, l1, s1, s0);  // X: PV_0(i), QK_1(i+1), SM_1(i)
+    phase(o1, P1, q0, S0n, S0c, P0, l0, s2, s0);  // Y: PV_1(i), QK_0(i+2), SM_0(i+1)
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const long long t0 = __builtin_amdgcn_s_memtime();
+  const long long r0 = __builtin_amdgcn_s_memrealtime();
+  for (int it = 0; it < steps; it += 2) {
+    iter(S0a, S0b, S1a, S1b, it);
+    iter(S0b, S0a, S1b, S1a, it + 1);
+  }
+  const long long t1 = __builtin_amdgcn_s_memtime();
+  const long long r1 = __builtin_amdgcn_s_memrealtime();
+  float s = l0 + l1;
+  for (int q = 0; q < 4; ++q)
+    for (int i = 0; i < 16; ++i) s += o0[q][i] + o1[q][i];
+  for (int i = 0; i < 16; ++i) s += (float)(S0a[0][i] + S1b[1][i]) + (float)(P0[i] ^ P1[i]);
+  sink[blockIdx.x * blockDim.x + tid] = s;
+  if (lane == 0) {
+    long long* o = out + (blockIdx.x * (blockDim.x >> 6) + (tid >> 6)) * 4;
+    o[0] = t0;
+    o[1] = t1;
+    o[2] = r0;
+    o[3] = r1;
+  }
+}
+
 // the board's power sensor (hwmon of the GPU's DRM device), first one that reads
 static std::string power_file() {
   for (const char* pat : {"/sys/class/drm/card*/device/hwmon/hwmon*/power1_input",
@@ -295,10 +408,16 @@ static double now_s() {
 }
 
 template <int T>
+static void launch(int cus, long long* d, float* sink, int steps) {
+  if constexpr (T == kPipeline64) hipLaunchKernelGGL(probe64, dim3(cus), dim3(256), 0, 0, d, sink, steps, 1.0f);
+  else hipLaunchKernelGGL((probe<T>), dim3(cus), dim3(512), 0, 0, d, sink, steps, 1.0f);
+}
+
+template <int T>
 static void run(int cus, double seconds, const std::string& pf, long long* d, float* sink) {
-  const int waves = 8, threads = 512, nw = cus * waves;
+  const int waves = T == kPipeline64 ? 4 : 8, nw = cus * waves;
   const int steps = kStepsPerLaunch[T];
-  hipLaunchKernelGGL((probe<T>), dim3(cus), dim3(threads), 0, 0, d, sink, 64, 1.0f);
+  launch<T>(cus, d, sink, 64);
   CHECK(hipDeviceSynchronize());
   std::atomic<bool> stop{false};
   std::vector<double> samples;
@@ -314,7 +433,7 @@ static void run(int cus, double seconds, const std::string& pf, long long* d, fl
   std::vector<double> cyc, clk;
   std::vector<long long> h(4 * nw);
   while (std::chrono::duration<double>(std::chrono::steady_clock::now() - tstart).count() < seconds) {
-    for (int k = 0; k < 8; ++k) hipLaunchKernelGGL((probe<T>), dim3(cus), dim3(threads), 0, 0, d, sink, steps, 1.0f);
+    for (int k = 0; k < 8; ++k) launch<T>(cus, d, sink, steps);
     CHECK(hipGetLastError());
     CHECK(hipDeviceSynchronize());
     launches += 8;
@@ -380,6 +499,7 @@ int main(int argc, char** argv) {
   run<kLds128>(cus, secs, pf, d, sink);
   run<kLds64>(cus, secs, pf, d, sink);
   run<kPipeline>(cus, secs, pf, d, sink);
+  run<kPipeline64>(cus, secs, pf, d, sink);
   run<kIdle>(cus, secs, pf, d, sink);
   CHECK(hipFree(d));
   CHECK(hipFree(sink));
