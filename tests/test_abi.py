@@ -169,6 +169,19 @@ def test_vtile_bytes_and_rejections(lib):
         assert rc != 0 and "invalid argument" in msg and needle in msg, msg
 
 
+def test_library_override_must_exist(hip_impl, monkeypatch, tmp_path):
+    """$TRIBENCH_SAGE_HIP_LIB naming no file is an error, not a silent fall
+    back to the in-tree library; naming a file selects it."""
+    missing = tmp_path / "no_such_lib.so"
+    monkeypatch.setenv("TRIBENCH_SAGE_HIP_LIB", str(missing))
+    with pytest.raises(RuntimeError, match="is not a file"):
+        hip_impl.library_path()
+    monkeypatch.delenv("TRIBENCH_SAGE_HIP_LIB")
+    default = hip_impl.library_path()
+    monkeypatch.setenv("TRIBENCH_SAGE_HIP_LIB", str(default))
+    assert hip_impl.library_path() == default
+
+
 def test_hip_variant_refuses_cpu_tensors(hip_impl):
     import torch
 

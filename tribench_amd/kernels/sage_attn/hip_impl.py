@@ -15,8 +15,9 @@ stream:
 There is no CPU or PyTorch fallback: without a ROCm device or without the
 library the call raises.  The module is loaded by file path (no parent
 package), so it finds the library from its own location:
-``$TRIBENCH_SAGE_HIP_LIB``, ``./libsage_attn.so`` next to this file, or
-``tribench_amd/lib/libsage_attn.so`` of this repository.
+``$TRIBENCH_SAGE_HIP_LIB`` when set (which must then name the file), else
+``./libsage_attn.so`` next to this file, or ``tribench_amd/lib/libsage_attn.so``
+of this repository.
 """
 from __future__ import annotations
 
@@ -44,12 +45,16 @@ _LIB = None
 
 
 def library_path() -> Path:
-    """Where the C-ABI library is looked up (first existing candidate)."""
+    """Where the C-ABI library is looked up: $TRIBENCH_SAGE_HIP_LIB when set
+    (it must name a file: an explicit choice never falls back to another
+    library), else the first existing default candidate."""
     here = Path(__file__).resolve().parent
-    cands = []
     env = os.environ.get("TRIBENCH_SAGE_HIP_LIB")
     if env:
-        cands.append(Path(env))
+        if not Path(env).is_file():
+            raise RuntimeError(f"sage_attn hip: TRIBENCH_SAGE_HIP_LIB={env} is not a file")
+        return Path(env)
+    cands = []
     cands.append(here / "libsage_attn.so")
     cands.append(here.parents[1] / "lib" / "libsage_attn.so")
     for c in cands:
