@@ -32,7 +32,9 @@
 //    of block j+1.  Blocks that need no mask take a path with no masking code.
 //  * The i32 score accumulator starts at the bit pattern of 2^23 + 2^22, so
 //    it reads as the float 12582912 + S (exact for |S| < 2^22 >= 127^2 * D):
-//    dequantisation and max-subtraction are one FMA per score.
+//    dequantisation and max-subtraction are one FMA per score, rounded once
+//    (the scale trimmed to 21 bits and the running max kept on a grid make
+//    its bias exact).
 //  * Lazy rescale: the running max moves only when a block's max exceeds it
 //    by more than tau (log2 units), so P stays bounded (SoftmaxCfg); the O
 //    rescale that a move needs is applied at the start of the next
@@ -261,6 +263,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const int ntile = (a.Nkv + kBN - 1) / kBN;
   const uint8_t* vtbase = static_cast<const uint8_t*>(a.v) + ((int64_t)b * a.Hkv + hk) * ntile * (int64_t)VTB;
 
+  // ---- the largest k scale of the head (INT8), for the grid of the running
+  // max below; loaded before every other load, so that waiting for it waits
+  // for nothing else
+  uint32_t ksc_max_bits = 0;  // positive floats order as their bit patterns
+  if constexpr (kI8) {
+    const float* ks = a.k_scale + ((int64_t)b * a.Hkv + hk) * a.nks;
+    for (int i = lane; i < a.nks; i += 64) ksc_max_bits = max(ksc_max_bits, __float_as_uint(ks[i]));
+  }
+
   // ---- Q, the B operand of S^T = K Q^T: row qa + n, bytes 32c + 16hh .. +16.
   // Rows past Nq read the last row; their results are never stored.
   v4i qreg[KC];
@@ -385,6 +396,23 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     wg_barrier();
   };
 
+  // ---- INT8 scores in one FMA, rounded once.  With the accumulator read as
+  // F = kMagicF + S, s * c - m = F * c - (kMagicF * c + m): the FMA gives the
+  // correctly rounded s * c - m when the bias kMagicF * c + m is exact.  It is
+  // when c has at most 21 significant bits (kMagicF = 3 * 2^22, so
+  // kMagicF * c has at most 23 and is an even multiple of its ulp), m is a
+  // multiple of mgrid = 4 ulp(kMagicF * c_max), c_max the lane's largest c, and
+  // |m| < kMagicF * c; with a larger |m| the bias is within an ulp of m.  c21
+  // truncates q_scale * k_scale to 21 bits (a relative change below 2^-21),
+  // and the running max moves on the grid, rounded up (P only shrinks, by
+  // less than 2^mgrid).  The grid is at most 1 (log2 units), which covers
+  // c_max up to about 0.16; beyond, the bias is within an ulp of
+  // kMagicF * c (scores that coarse make the softmax nearly one-hot).
+  // Rounded once per block instead, the bias would shift each block's scores
+  // by up to 0.75 c log2 units, differently from block to block.
+  auto c21 = [](float c) __attribute__((always_inline)) { return __uint_as_float(__float_as_uint(c) & ~3u); };
+  float mgrid = 1.0f, mgrid_inv = 1.0f;  // set once Q's scale is known
+
   // ---- accumulators and softmax state
   v16f oacc[DT];
 #pragma unroll
@@ -476,7 +504,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                         __attribute__((always_inline)) {
     const int k0 = j * kBN;
     const int qrow = qa + n;
-    const float c = kI8 ? qsc * kx : a.qk_mul;
+    const float c = kI8 ? c21(qsc * kx) : a.qk_mul;
     float mblk;
     if constexpr (kI8) {
       int x[32];
@@ -510,14 +538,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     }
     // lazy max update (per q column; both lane halves agree)
     const bool need = mblk > m_use + SoftmaxCfg<PVM>::kTau;
-    const float mnew = need ? mblk : m_use;
+    // INT8: m = mnew - kShift on the grid, rounded up (P only shrinks)
+    const float mup = kI8 ? __builtin_ceilf((mblk - SoftmaxCfg<PVM>::kShift) * mgrid_inv) * mgrid + SoftmaxCfg<PVM>::kShift
+                          : mblk;
+    const float mnew = need ? mup : m_use;
     const float alpha = need ? __builtin_amdgcn_exp2f(m_use - mnew) : 1.0f;
     m_use = mnew;
     lsum *= alpha;
     alpha_o *= alpha;
     pend |= __builtin_amdgcn_ballot_w64(need) != 0;
     const float m = (mnew == -INFINITY ? 0.0f : mnew) - SoftmaxCfg<PVM>::kShift;
-    // INT8: S reads as the float 2^23 + 2^22 + S, so S*c - m = that*c - bias
+    // INT8: S reads as the float 2^23 + 2^22 + S, so S*c - m = that*c - bias,
+    // the bias exact (see c21)
     const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
     // fp16 P: the row sum adds the fp16 values the P.V MFMAs consume, in a
     // packed fp16 tree (15 v_pk_add_f16 instead of 32 fp32 adds; P <= 2^kTau,
@@ -574,13 +606,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   // largest term), so if every lane's sum is at most 2^(kTau + kShift - 1)
   // the block max is within kTau of m_use and P and the new lsum are the
   // ones softmax() computes, bit for bit; nothing else changes.  The margin
-  // covers the rounding of the INT8 bias (error below 0.75 * c, so the
-  // shortcut is exact for c < 4/3); an m_use of -inf (sums of +inf) and NaN
+  // covers the rounding of the scores (the INT8 bias is exact, or within an
+  // ulp of m: see c21); an m_use of -inf (sums of +inf) and NaN
   // scores fail the test.  Otherwise softmax() redoes the block from the
   // untouched S.  Not used for FP8 P: with kShift = 6 the sums of a typical
   // block exceed the bound.
   auto softmax_fast_on = [&](int j, uint32_t (&P)[PW], const SAcc (&Sx)[2], float kx) __attribute__((always_inline)) {
-    const float c = kI8 ? qsc * kx : a.qk_mul;
+    const float c = kI8 ? c21(qsc * kx) : a.qk_mul;
     const float m = m_use - SoftmaxCfg<PVM>::kShift;
     const float bias = kI8 ? __builtin_fmaf(kMagicF, c, m) : m;
     constexpr bool kSumF16 = PVM == SAGE_PV_F16;
@@ -782,6 +814,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   sync_tiles(nkb > 2);
   if (jmax >= 0) qk(0, 0);
 
+  if constexpr (kI8) {  // mgrid = 4 ulp(kMagicF * c_max): exponent field of that product - 21,
+    // at least 2^-23 (a coarser grid keeps the bias exact; with a zero scale
+    // the grid's inverse times m - kShift must not overflow) and at most 1
+    const float cmax = c21(qsc * __uint_as_float(wave_max_u32(ksc_max_bits)));
+    const int e = (int)((__float_as_uint(kMagicF * cmax) >> 23) & 0xFF);
+    const int eg = min(max(e - 21, 104), 127);
+    mgrid = __uint_as_float((uint32_t)eg << 23);
+    mgrid_inv = __uint_as_float((uint32_t)(254 - eg) << 23);
+  }
   const int j_fast = min(min(nfull, jmax), min(nkb, a.Nkv / kBN) - 3);  // tile j+3 whole
   generic_iter(0);
   int j = 1;
