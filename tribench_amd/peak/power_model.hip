@@ -25,10 +25,17 @@
 //   pipeline64     the same data flow with 64 query rows per wave and one
 //                  wave per SIMD (4-wave work-groups; issue_model.hip's
 //                  pipeline64): half the LDS operand bytes per block
+//   pipeline16     the pipeline's data flow on the 16x16 MFMA shapes
+//                  (i32_16x16x64_i8, f32_16x16x32_f16): the wave's 32 rows
+//                  as two groups of 16, each LDS operand read feeding both
+//                  groups' MFMAs, so the same LDS bytes and twice the MFMAs
 // Output: one JSON line per test (cycles per step, clock, board watts,
 // instructions of the class per second on the device).
 //
-// usage: power_model [seconds per test]      run the tests (default 3)
+// usage: power_model [seconds per test] [name prefix]
+//                                             run the tests (default 3 s; with
+//                                             a prefix, only the tests whose
+//                                             name starts with it, and idle)
 //        power_model --sample SECONDS         print the board power every 100 ms
 //                                             (no GPU use: for timing another program)
 #include <hip/hip_runtime.h>
@@ -65,7 +72,7 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr int kLds = 120 * 1024;
 enum Test { kIdle, kMfmaI8, kMfmaF16, kMfmaI8s, kMfmaF16s, kMfmaF8, kFma, kExp, kPkAdd, kLds128, kLds64, kPipeline,
-            kPipeline64 };
+            kPipeline64, kPipeline16 };
 static const char* kName[] = {"idle(s_sleep)",
                               "mfma_i32_32x32x32_i8",
                               "mfma_f32_32x32x16_f16",
@@ -78,12 +85,13 @@ static const char* kName[] = {"idle(s_sleep)",
                               "ds_read_b128",
                               "ds_read_b64",
                               "pipeline(attention iteration)",
-                              "pipeline64(64 rows per wave, 1 wave per SIMD)"};
+                              "pipeline64(64 rows per wave, 1 wave per SIMD)",
+                              "pipeline16(16x16 MFMA shapes)"};
 // instructions of the measured class per wave and step
-static const int kPerStep[] = {0, 8, 8, 8, 8, 8, 16, 16, 16, 24, 24, 24, 48};
+static const int kPerStep[] = {0, 8, 8, 8, 8, 8, 16, 16, 16, 24, 24, 24, 48, 48};
 // steps per launch: 5-15 ms each
 static const int kStepsPerLaunch[] = {20000, 60000, 60000, 60000, 60000, 30000, 60000, 60000, 60000, 25000, 25000, 8000,
-                                      4000};
+                                      4000, 8000};
 
 template <int T>
 __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int steps, float seed) {
@@ -176,6 +184,80 @@ __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int st
     asm volatile("" ::: "memory");
   };
 
+  // 16x16 pipeline state: O as [D chunk of 16][row group], S as [key chunk
+  // of 16][row group], P as [32-key chunk][row group][4 words]
+  v4f o16[16] = {};
+  v4i S16a[8], S16b[8];
+  uint32_t P16a[16], P16b[16];
+  float lsum16[2] = {0.0f, 0.0f};
+  if constexpr (T == kPipeline16) {
+    for (int j = 0; j < 8; ++j)
+      for (int v = 0; v < 4; ++v) {
+        S16a[j][v] = magic + (4 * j + v) * 37 + lane;
+        S16b[j][v] = magic - (4 * j + v) * 41 - lane;
+      }
+    for (int w = 0; w < 16; ++w) {
+      P16a[w] = Pa[w];
+      P16b[w] = Pb[w];
+    }
+  }
+  // one attention iteration on the 16x16 shapes: 32 P.V MFMAs (A = a 16 D x
+  // 32 key V fragment from LDS, shared by both row groups; B = P), 16 QK MFMAs
+  // (A = a 16 key x 64 D K fragment from LDS, shared by both row groups; B =
+  // Q registers) into the other S buffer, the softmax of the current S (32
+  // FMA, 32 exp, 16 cvt, 14 packed adds, 2 dot2), a barrier
+  auto iter16 = [&](const uint32_t (&Pp)[16], const v4i (&Sc)[8], uint32_t (&Pc)[16], v4i (&Sn)[8], int it)
+                    __attribute__((always_inline)) {
+    const int base = (it & 3) * 24576;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const v4i va = *reinterpret_cast<const v4i*>(lds + base + voff + 1024 * (2 * dt + kk));
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+          const v4i pb = {(int)Pp[8 * kk + 4 * g], (int)Pp[8 * kk + 4 * g + 1], (int)Pp[8 * kk + 4 * g + 2],
+                          (int)Pp[8 * kk + 4 * g + 3]};
+          o16[2 * dt + g] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, va),
+                                                                   __builtin_bit_cast(v8h, pb), o16[2 * dt + g], 0, 0, 0);
+        }
+      }
+    const v4i mg4 = {magic, magic, magic, magic};
+#pragma unroll
+    for (int dc = 0; dc < 2; ++dc)
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const v4i ka = *reinterpret_cast<const v4i*>(lds + base + koff + 1024 * (2 * kc + dc));
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+          Sn[2 * kc + g] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ka, op[2 * g + dc], dc == 0 ? mg4 : Sn[2 * kc + g], 0, 0, 0);
+      }
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        float p[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(__int_as_float(Sc[2 * (2 * kk + v / 4) + g][v & 3]), csc, -bias));
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          Pc[8 * kk + 4 * g + w] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){p[2 * w], p[2 * w + 1]}, h2));
+      }
+      h2 hs[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) hs[w] = __builtin_bit_cast(h2, Pc[4 * g + w]) + __builtin_bit_cast(h2, Pc[8 + 4 * g + w]);
+      hs[0] = hs[0] + hs[2];
+      hs[1] = hs[1] + hs[3];
+      hs[0] = hs[0] + hs[1];
+      lsum16[g] = __builtin_amdgcn_fdot2(hs[0], (h2){(_Float16)1.0f, (_Float16)1.0f}, lsum16[g], false);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
   const long long t0 = __builtin_amdgcn_s_memtime();
   const long long r0 = __builtin_amdgcn_s_memrealtime();
   for (int it = 0; it < steps; ++it) {
@@ -240,6 +322,10 @@ __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int st
       }
       acc4.x ^= a2.x;
       acc4.y ^= a2.y;
+    } else if constexpr (T == kPipeline16) {  // as below, on the 16x16 shapes
+      iter16(P16a, S16a, P16b, S16b, it);
+      iter16(P16b, S16b, P16a, S16a, it + 1);
+      ++it;
     } else {  // two iterations per trip swap the S and P buffers (steps iterations in all)
       iter(Pa, Sa, Pb, Sb, it);
       iter(Pb, Sb, Pa, Sa, it + 1);
@@ -255,6 +341,11 @@ __global__ __launch_bounds__(512) void probe(long long* out, float* sink, int st
     for (int i = 0; i < 4; ++i) s += cs[q][i] + (float)cis[q][i];
   }
   for (int i = 0; i < 16; ++i) s += (float)(Sa[0][i] + Sb[1][i]) + (float)(Pa[i] ^ Pb[i]);
+  if constexpr (T == kPipeline16) {
+    s += lsum16[0] + lsum16[1];
+    for (int j = 0; j < 16; ++j) s += o16[j][0] + o16[j][3] + (float)(P16a[j] ^ P16b[j]);
+    for (int j = 0; j < 8; ++j) s += (float)(S16a[j][1] + S16b[j][2]);
+  }
   sink[blockIdx.x * blockDim.x + tid] = s;
   if (lane == 0) {
     long long* o = out + (blockIdx.x * (blockDim.x >> 6) + (tid >> 6)) * 4;
@@ -414,7 +505,8 @@ static void launch(int cus, long long* d, float* sink, int steps) {
 }
 
 template <int T>
-static void run(int cus, double seconds, const std::string& pf, long long* d, float* sink) {
+static void run(int cus, double seconds, const std::string& pf, long long* d, float* sink, const char* only) {
+  if (only && T != kIdle && std::strncmp(kName[T], only, std::strlen(only)) != 0) return;
   const int waves = T == kPipeline64 ? 4 : 8, nw = cus * waves;
   const int steps = kStepsPerLaunch[T];
   launch<T>(cus, d, sink, 64);
@@ -477,6 +569,7 @@ int main(int argc, char** argv) {
     return 0;
   }
   const double secs = argc > 1 ? std::atof(argv[1]) : 3.0;
+  const char* only = argc > 2 ? argv[2] : nullptr;
   hipDeviceProp_t p;
   CHECK(hipGetDeviceProperties(&p, 0));
   std::printf("{\"device\": \"%s\", \"arch\": \"%s\", \"compute_units\": %d, \"power_file\": \"%s\", \"watts_now\": %.1f}\n",
@@ -487,20 +580,21 @@ int main(int argc, char** argv) {
   float* sink;
   CHECK(hipMalloc(&d, sizeof(long long) * 4 * cus * 8));
   CHECK(hipMalloc(&sink, sizeof(float) * cus * 512));
-  run<kIdle>(cus, secs, pf, d, sink);
-  run<kMfmaI8>(cus, secs, pf, d, sink);
-  run<kMfmaF16>(cus, secs, pf, d, sink);
-  run<kMfmaI8s>(cus, secs, pf, d, sink);
-  run<kMfmaF16s>(cus, secs, pf, d, sink);
-  run<kMfmaF8>(cus, secs, pf, d, sink);
-  run<kFma>(cus, secs, pf, d, sink);
-  run<kExp>(cus, secs, pf, d, sink);
-  run<kPkAdd>(cus, secs, pf, d, sink);
-  run<kLds128>(cus, secs, pf, d, sink);
-  run<kLds64>(cus, secs, pf, d, sink);
-  run<kPipeline>(cus, secs, pf, d, sink);
-  run<kPipeline64>(cus, secs, pf, d, sink);
-  run<kIdle>(cus, secs, pf, d, sink);
+  run<kIdle>(cus, secs, pf, d, sink, only);
+  run<kMfmaI8>(cus, secs, pf, d, sink, only);
+  run<kMfmaF16>(cus, secs, pf, d, sink, only);
+  run<kMfmaI8s>(cus, secs, pf, d, sink, only);
+  run<kMfmaF16s>(cus, secs, pf, d, sink, only);
+  run<kMfmaF8>(cus, secs, pf, d, sink, only);
+  run<kFma>(cus, secs, pf, d, sink, only);
+  run<kExp>(cus, secs, pf, d, sink, only);
+  run<kPkAdd>(cus, secs, pf, d, sink, only);
+  run<kLds128>(cus, secs, pf, d, sink, only);
+  run<kLds64>(cus, secs, pf, d, sink, only);
+  run<kPipeline>(cus, secs, pf, d, sink, only);
+  run<kPipeline64>(cus, secs, pf, d, sink, only);
+  run<kPipeline16>(cus, secs, pf, d, sink, only);
+  run<kIdle>(cus, secs, pf, d, sink, only);
   CHECK(hipFree(d));
   CHECK(hipFree(sink));
   return 0;
