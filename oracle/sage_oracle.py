@@ -153,7 +153,8 @@ def e4m3_encode(x):
     af = a.view(np.float32)
     code = np.zeros(x.shape, dtype=np.uint32)
     sub = af < np.float32(2.0 ** -6)
-    sub_code = np.rint(np.minimum(af, np.float32(1.0)) * np.float32(512.0)).astype(np.uint32)
+    # only the subnormal lanes enter the cast (NaN, inf and large values would not fit uint32)
+    sub_code = np.rint(np.where(sub, af, np.float32(0.0)) * np.float32(512.0)).astype(np.uint32)
     code = np.where(sub, sub_code, code)
     e = (a >> np.uint32(23)).astype(np.int64) - 127 + 7
     m = a & np.uint32(0x7FFFFF)
