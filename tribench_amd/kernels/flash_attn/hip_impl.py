@@ -34,6 +34,7 @@ _H = _sage_hip()
 _PV_OF = {torch.float16: "fp16", torch.bfloat16: "bf16"}
 
 
+@_H._on_tensor_device
 def run(q, k, v, causal=False, sm_scale=None, *, tensor_layout="HND", **kw):
     """FlashAttention forward on MI355X: q [B,Hq,Nq,D], k/v [B,Hkv,Nkv,D]
     (HND, or NHD with ``tensor_layout``), fp16 or bf16; returns o with q's

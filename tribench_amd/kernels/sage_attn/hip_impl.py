@@ -22,6 +22,7 @@ of this repository.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 from pathlib import Path
 
@@ -147,6 +148,24 @@ def _stream(device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+def _on_tensor_device(fn):
+    """Run ``fn`` with the device of its first tensor argument current.
+
+    The library launches on torch's current stream of that device and keeps
+    per-device state (the no-allocation entry point's scratch array, found
+    with hipGetDevice), so the data's device must be the current one
+    whatever device the caller left current.
+    """
+    @functools.wraps(fn)
+    def wrapper(*args, **kwargs):
+        dev = next((a.device for a in args if isinstance(a, torch.Tensor)), None)
+        if dev is None or dev.type != "cuda":
+            return fn(*args, **kwargs)
+        with torch.cuda.device(dev):
+            return fn(*args, **kwargs)
+    return wrapper
+
+
 def _check_inputs(q, k, v, layout):
     for name, t in (("q", q), ("k", k), ("v", v)):
         if not isinstance(t, torch.Tensor):
@@ -176,6 +195,7 @@ def _empty_like_layout(t: torch.Tensor, dtype) -> torch.Tensor:
     return torch.empty_like(t, dtype=dtype, memory_format=torch.preserve_format)
 
 
+@_on_tensor_device
 def vtiles(v, pv_dtype="fp16", v_scale=None, *, tensor_layout="HND"):
     """V in the attention kernel's tile layout (uint8 buffer), converted to
     the P.V type: the counterpart of the reference's v.to(torch.float16)
@@ -196,6 +216,7 @@ def vtiles(v, pv_dtype="fp16", v_scale=None, *, tensor_layout="HND"):
     return out
 
 
+@_on_tensor_device
 def prepass(q, k, v=None, sm_scale=None, *, blkq=128, blkk=64, q_sub=None, smooth_k=True,
             v_fp8=False, pv_dtype=None, quant_q=True, tensor_layout="HND", static_scratch=False):
     """Run the HIP pre-pass; returns a dict of device tensors.
@@ -292,6 +313,7 @@ def fuse_q_default(head_dim):
     return head_dim == 128
 
 
+@_on_tensor_device
 def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
                   fuse_q=None, tensor_layout="HND", **kw):
     """The pre-pass of :func:`run` alone, with run's arguments (the harness
@@ -303,6 +325,7 @@ def prepass_stage(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gr
                    tensor_layout=tensor_layout)
 
 
+@_on_tensor_device
 def per_block_int8(q, k, km=None, BLKQ=128, BLKK=64, sm_scale=None, tensor_layout="HND"):
     """HIP counterpart of per_block_int8 (triton_impl.py:35-82).
 
@@ -330,6 +353,7 @@ def _tiles_for(pre, v, pv_dtype, B, Hkv, Nkv, D, tensor_layout):
     return vt
 
 
+@_on_tensor_device
 def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=128, blkk=64, tensor_layout="HND",
               out=None):
     """Launch the fused attention kernel on the outputs of :func:`prepass`.
@@ -355,6 +379,7 @@ def attention(q, k, v, pre, causal=False, *, pv_dtype="fp16", q_sub=128, blkq=12
     return o
 
 
+@_on_tensor_device
 def attention_q(q, k, v, pre, causal=False, sm_scale=None, *, pv_dtype="fp16", q_sub=128, blkk=64,
                 tensor_layout="HND", out=None, q8_out=None, q_scale_out=None):
     """The fused attention with the Q quantization of the pre-pass done in its
@@ -383,6 +408,7 @@ def attention_q(q, k, v, pre, causal=False, sm_scale=None, *, pv_dtype="fp16", q
     return o
 
 
+@_on_tensor_device
 def run(q, k, v, causal=False, sm_scale=None, *, pv_dtype="fp16", q_gran="block", smooth_k=True,
         fuse_q=None, tensor_layout="HND", return_intermediates=False, **kw):
     """SageAttention forward on MI355X: INT8 QK^T, online softmax, P.V.
