@@ -63,11 +63,16 @@ def _first_mismatch(name, got, want):
     return f"{name}: {len(diff)} mismatches, first at {list(i)}: got {got[i]} want {want[i]}"
 
 
-@pytest.mark.parametrize("name", FULL)
-def test_fullsize_quantization_and_output(name, pack_ref, hip_impl, gpu_device):
+# every configuration with bf16 inputs (the benchmark configurations' type), and configuration 2
+# with fp16 inputs too (the reference harness's default dtype)
+PARAMS = [(n, torch.bfloat16) for n in FULL] + [(FULL[0], torch.float16)]
+
+
+@pytest.mark.parametrize("name,dtype", PARAMS, ids=[f"{n}-{str(d)[6:]}" for n, d in PARAMS])
+def test_fullsize_quantization_and_output(name, dtype, pack_ref, hip_impl, gpu_device):
     case = _case(name)
-    print(f"[fullsize] {name} {case}", flush=True)
-    inp = pack_ref.make_inputs(case, "cpu", 0, torch.bfloat16)
+    print(f"[fullsize] {name} {dtype} {case}", flush=True)
+    inp = pack_ref.make_inputs(case, "cpu", 0, dtype)
     q, k, v = (inp[x].to(gpu_device) for x in ("q", "k", "v"))
     causal = inp["causal"]
     pv = case.get("pv_dtype", "fp16")
