@@ -41,3 +41,32 @@ def test_cli_run_records_rocm_env_and_roofline_columns(tmp_path, gpu_device, cap
     report = (run_json.parent / "report.html").read_text()
     assert "gfx950" in report and "cpu_ref" in report and "<svg" in report
     assert "<th>roofline</th>" in report and "<th>pre-pass GB/s</th>" in report and "<th>eff. TOPS</th>" in report
+
+
+def test_cli_test_command_on_both_packs(gpu_device, capsys):
+    """`test` (tribench/cli.py's correctness command) on the GPU: every case of
+    a small selection passes the pack's gate, for the INT8 and the flash pack."""
+    for kernel, cases, dtype in (("sage_attn", "cfg1_b1h2n256d64", "bf16"), ("flash_attn", "s4k_d64", "fp16")):
+        print(f"[harness-test] cli test {kernel} {cases} {dtype}", flush=True)
+        with pytest.raises(SystemExit) as e:
+            cli.main(["test", "--kernel", kernel, "--cases", cases, "--dtype", dtype, "--device", "cuda:0"])
+        printed = capsys.readouterr().out
+        assert e.value.code == 0 and "FAIL" not in printed, printed
+
+
+def test_cli_run_with_the_hip_graph_timer(tmp_path, gpu_device, capsys):
+    """`run --timer hip_graph`: the call captured into a HIP graph and its
+    replays timed (harness/bench.py); the row still passes its correctness
+    check, which runs the call eagerly."""
+    out_dir = tmp_path / "res"
+    print("[harness-graph] cli run sage_attn cfg1_b1h2n256d64 bf16 --timer hip_graph", flush=True)
+    with pytest.raises(SystemExit) as e:
+        cli.main(["run", "--kernel", "sage_attn", "--cases", "cfg1_b1h2n256d64", "--dtype", "bf16",
+                  "--device", "cuda:0", "--warmup-ms", "5", "--rep-ms", "20", "--timer", "hip_graph",
+                  "--no-plots", "--output-dir", str(out_dir)])
+    printed = capsys.readouterr().out
+    assert e.value.code == 0, printed
+    (run_json,) = out_dir.glob("*/run.json")
+    (h,) = [r for r in json.loads(run_json.read_text())["results"] if r["variant"] == "hip"]
+    assert h["correctness"]["passed"] and h["timer_backend"] == "hip_graph", h
+    assert h["latency_ms_p50"] > 0, h
