@@ -4,7 +4,10 @@ Every ``csrc/*.hip`` translation unit is compiled with ``hipcc
 --offload-arch=gfx950`` and linked into one shared library.  Builds in-tree
 (the ``.so`` travels with the source tree) and always recompiles.
 
-Usage: ``python -m tribench_amd.build [-j N]``.
+Usage: ``python -m tribench_amd.build [-j N] [--peak]``.  ``--peak`` also
+builds the roofline measurement programs of ``tribench_amd/peak`` (MFMA and
+HBM peaks); the library and the device checks the GPU tests run are always
+built.
 """
 from __future__ import annotations
 
@@ -65,8 +68,10 @@ def _compile(src: Path, obj: Path) -> None:
         print("\n".join(msgs), file=sys.stderr)
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> Path:
-    """Compile every HIP unit for gfx950 and link ``libsage_attn.so``."""
+def build(jobs: int | None = None, verbose: bool = True, peak: bool = False) -> Path:
+    """Compile every HIP unit for gfx950 and link ``libsage_attn.so``, then
+    the device checks of ``tests/native`` (and, with ``peak``, the roofline
+    measurement programs)."""
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
@@ -86,25 +91,34 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
-    build_peak(verbose)
+    build_checks(verbose)
+    if peak:
+        build_peak(verbose)
     return LIB
 
 
-# Measurement programs (tribench_amd/peak/*.hip -> tribench_amd/lib/<stem>):
-# mfma_peak measures the dense MFMA peaks the roofline figures use,
-# issue_model how a SIMD overlaps the attention loop's instruction mix,
-# hbm_peak what streaming kernels move through HBM.  The device checks of
-# tests/native/*.hip (run by the GPU tests) are built the same way, with the
-# pre-pass's floating-point flags.
+# Roofline measurement programs (tribench_amd/peak/*.hip ->
+# tribench_amd/lib/<stem>): mfma_peak measures the dense MFMA peaks the
+# roofline figures divide by, hbm_peak what streaming kernels move through
+# HBM.  The device checks of tests/native/*.hip (run by the GPU tests) are
+# built the same way, with the pre-pass's floating-point flags.
 PEAK_DIR = PKG / "peak"
 CHECK_DIR = PKG.parent / "tests" / "native"
 
 
+def build_checks(verbose: bool = True) -> list[Path]:
+    """The device checks the GPU tests run (``tests/native/*.hip``)."""
+    return _build_exes([(s, ["-ffp-contract=off"]) for s in sorted(CHECK_DIR.glob("*.hip"))], verbose)
+
+
 def build_peak(verbose: bool = True) -> list[Path]:
+    """The roofline measurement programs (``tribench_amd/peak/*.hip``)."""
+    return _build_exes([(s, []) for s in sorted(PEAK_DIR.glob("*.hip"))], verbose)
+
+
+def _build_exes(srcs: list[tuple[Path, list[str]]], verbose: bool) -> list[Path]:
     LIBDIR.mkdir(exist_ok=True)
     exes = []
-    srcs = [(s, []) for s in sorted(PEAK_DIR.glob("*.hip"))]
-    srcs += [(s, ["-ffp-contract=off"]) for s in sorted(CHECK_DIR.glob("*.hip"))]
     for src, extra in srcs:
         exe = LIBDIR / src.stem
         tmp = exe.with_name(exe.name + ".tmp")
@@ -122,8 +136,9 @@ def build_peak(verbose: bool = True) -> list[Path]:
 def main(argv: list[str] | None = None) -> int:
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("-j", "--jobs", type=int, default=None)
+    p.add_argument("--peak", action="store_true", help="also build the roofline measurement programs")
     args = p.parse_args(argv)
-    build(args.jobs)
+    build(args.jobs, peak=args.peak)
     return 0
 
 
