@@ -187,8 +187,9 @@ def test_case_grid_and_filters():
     assert [c.dtype for c in case_grid(meta, cases=["s4k_d64"], dtypes=["fp32", "bf16", "fp32"])] == ["fp32", "bf16"]
     with pytest.raises(ValueError, match="no dtype 'fp64'"):
         case_grid(meta, dtypes=["fp64"])
-    with pytest.raises(ValueError, match="no case 'nope'"):
-        case_grid(meta, cases=["nope"])
+    # case names a pack does not offer are passed over (tribench/gen.py:19-20)
+    assert case_grid(meta, cases=["nope"]) == []
+    assert [c.name for c in case_grid(meta, cases=["nope", "s4k_d64"], dtypes=["bf16"])] == ["s4k_d64"]
 
 
 def test_seeded_inputs(pack_ref):
@@ -337,6 +338,26 @@ def test_cli_test_on_fake_packs(tmp_path, monkeypatch, capsys, body, code, needl
         cli.main(["test", "--kernel", "fake", "--device", "cpu"])
     out = capsys.readouterr().out
     assert e.value.code == code and needle in out
+
+
+def test_cli_test_all_packs_with_a_case_of_one_pack(tmp_path, monkeypatch, capsys):
+    """--kernel all with a case name only one pack offers: the other pack
+    runs no case and the command passes."""
+    kdir = _fake_pack(tmp_path, "def run(x):\n    return x * 2\n")
+    other = kdir / "other"
+    other.mkdir()
+    for f in ("reference.py", "impl.py"):
+        (other / f).write_text((kdir / "fake" / f).read_text())
+    meta = json.loads((kdir / "fake" / "meta.json").read_text())
+    meta["name"] = "other"
+    meta["cases"] = [{"name": "big", "N": 64}]
+    (other / "meta.json").write_text(json.dumps(meta))
+    monkeypatch.setattr("tribench_amd.harness.packs.KERNELS_DIR", kdir)
+    with pytest.raises(SystemExit) as e:
+        cli.main(["test", "--kernel", "all", "--cases", "small", "--device", "cpu"])
+    out = capsys.readouterr().out
+    assert e.value.code == 0, out
+    assert "--- other (0 case(s)) ---" in out and "PASS  small" in out and "SKIP" not in out
 
 
 def test_cli_test_hip_variant_without_gpu_fails_loudly(capsys):

@@ -48,9 +48,12 @@ def _subset(what: str, pack: str, wanted: Sequence[str] | None, offered: Sequenc
 def case_grid(meta: KernelMeta, *, cases: Sequence[str] | None = None, dtypes: Sequence[str] | None = None,
               layouts: Sequence[str] | None = None) -> list[Case]:
     """The grid of ``meta``'s cases, dtypes and layouts, narrowed to the
-    requested names (each of which the pack must offer)."""
+    requested names.  Case names the pack does not offer are passed over
+    (one command line may name cases of several packs, as
+    tribench/gen.py:19-20 allows); a requested dtype or layout the pack does
+    not support is a ValueError."""
     defs = {c.name: c for c in meta.cases}
-    names = _subset("case", meta.name, cases, list(defs))
+    names = [n for n in defs if n in set(cases)] if cases else list(defs)
     dts = _subset("dtype", meta.name, dtypes, meta.supported.dtypes)
     lays = _subset("layout", meta.name, layouts, meta.supported.layouts)
     return [Case(name=n, params=dict(defs[n].params), dtype=d, layout=lay)
