@@ -11,7 +11,8 @@ Checks, as in test_gpu_fullsize.py:
    triton_impl.py:7-33, 35-82, and the K channel mean), as ``run`` returns
    them;
 2. sampled query rows against the exact emulation of the same INT8 data,
-   within 2e-3 + 2^-8 |emu| (the bf16 rounding of the output);
+   within 2e-3 + 2^-8 |emu| (the bf16 rounding of the output), the part
+   beyond half an ulp of the bf16 output within 0.3 of that;
 3. the north star's gate against the fp32 reference (reference.py:15-24) on
    the GPU: max-abs <= 2e-2 (rows >= 128 when causal) and cosine >= 0.999.
 """
@@ -22,6 +23,7 @@ import pytest
 import torch
 
 from oracle import sage_oracle as O
+from parity_util import emulation_split, split_line
 
 pytestmark = pytest.mark.gpu
 
@@ -33,12 +35,6 @@ CASES = [
     ("n65537_d128_causal", dict(batch_size=1, num_heads=2, seq_len=65537, head_dim=128, k_offset_std=4.0), True),
 ]
 SAMPLE = 128
-
-
-def _rows(N, seed):
-    rng = np.random.default_rng(seed)
-    return np.unique(np.concatenate([np.arange(SAMPLE), np.arange(N - SAMPLE, N),
-                                     rng.choice(N, size=SAMPLE, replace=False)]))
 
 
 @pytest.mark.parametrize("name,case,causal", CASES, ids=[c[0] for c in CASES])
@@ -64,20 +60,15 @@ def test_long_sequence(name, case, causal, pack_ref, hip_impl, gpu_device):
             assert np.array_equal(got[key][:, hk:hk + 1], want[key]), f"{name} hk{hk}: {key}"
 
     # 2. sampled rows of the first and last head against the exact emulation
-    got_o = o.float().cpu().numpy()
+    want_o = pack_ref.ref(q, k, v, causal=causal)
     for h in (0, Hq - 1):
-        hk = h // G
-        rows = _rows(N, seed=h)
-        emu = O.sage_emulate(got["q8"][:, h:h + 1], got["q_scale"][:, h:h + 1], got["k8"][:, hk:hk + 1],
-                             got["k_scale"][:, hk:hk + 1], vn[:, hk:hk + 1], causal=causal, rows=rows)[0, 0]
-        e = np.abs(got_o[0, h, rows].astype(np.float64) - emu)
-        bound = 2e-3 + 2.0 ** -8 * np.abs(emu)
-        print(f"  h={h}: {len(rows)} rows vs emulation max_abs={e.max():.3e} worst e/bound={(e / bound).max():.3f}",
-              flush=True)
-        assert np.isfinite(got_o[0, h, rows]).all() and (e <= bound).all(), f"{name} h{h}"
+        sp = emulation_split(o, want_o, got, vn, 0, h, G, causal=causal, q_sub=hip_impl.q_sub_of("block"),
+                             sample=SAMPLE)
+        print("  " + split_line(f"{name} h={h}", sp), flush=True)
+        assert np.isfinite(sp["got"]).all() and (sp["err"] <= sp["bound"]).all(), f"{name} h{h}"
+        assert sp["arith_ratio"] <= 0.3, f"{name} h{h}"
 
     # 3. the north star's gate against the fp32 reference
-    want_o = pack_ref.ref(q, k, v, causal=causal)
     of = o.float()
     diff = (of - want_o).abs()
     max_abs = float(diff[:, :, 128:].max() if causal else diff.max())
