@@ -21,8 +21,17 @@ the V tiles written once; Q too where the pre-pass quantizes it) as a
 fraction of the published 8 TB/s (``hbm_frac``) and of a plain 1 GiB device
 copy timed on the same box first (``copy_gbps``, ``frac_of_copy``).
 
+Before the W warmup steps of each configuration the step runs untimed for
+``--settle-ms`` of wall time (default 200 ms, TriBench's own warmup time,
+tribench/cli.py:47 and tribench/bench.py:119): the GPU's clock ramps up from
+idle over the first ~25 steps of this workload (0.9-1.07 ms per attention
+launch against 0.81 ms settled), so without it a short run times the ramp.
+``--settle-ms 0`` gives the W-steps-only warmup; the JSON line reports the
+settle steps run.
+
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2] [--also cfg3|none]
                   [--no-cpu-baseline] [--copy-probe-gib G] [--q-quant auto|prologue|pre-pass]
+                  [--settle-ms MS]
 """
 from __future__ import annotations
 
@@ -67,28 +76,16 @@ def _load(stem: str):
 
 
 def _traffic_from_profiles(cfg: str):
-    """HBM bytes per attention launch of a configuration, measured with
-    rocprofv3 FETCH_SIZE / WRITE_SIZE (the committed summary of that
-    configuration; None if there is none)."""
-    f = ROOT / "profiles" / f"attn_fwd_{cfg}_hbm_traffic.md"
+    """HBM bytes per attention launch of a configuration and the file they
+    come from: measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (copy-
+    calibrated) in the committed summary of that configuration, not in this
+    run; (None, None) if there is none."""
+    rel = f"profiles/attn_fwd_{cfg}_hbm_traffic.md"
+    f = ROOT / rel
     if not f.exists():
-        return None
+        return None, None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", f.read_text())
-    return float(m.group(1)) if m else None
-
-
-def cpu_model() -> str:
-    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
-        pass
-    import platform
-
-    return platform.processor() or "unknown"
+    return (float(m.group(1)), rel) if m else (None, None)
 
 
 def cpu_baseline(R, case, budget_s: float = 15.0) -> dict:
@@ -96,6 +93,7 @@ def cpu_baseline(R, case, budget_s: float = 15.0) -> dict:
     workload, cycling through them until ``budget_s`` of wall time is spent;
     TOPS by the metric's formula on the slices done."""
     from oracle import sage_oracle as O
+    from tribench_amd.harness.env import cpu_model
 
     threads = len(os.sched_getaffinity(0))
     try:
@@ -141,6 +139,9 @@ def main(argv=None) -> int:
     ap.add_argument("--q-quant", default="auto", choices=["auto", "prologue", "pre-pass"],
                     help="where Q is quantized: as hip_impl.run does by default (auto), in the attention "
                          "kernel's prologue, or in the pre-pass")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed steps for this much wall time before the warmup steps of each configuration "
+                         "(the clock's ramp from idle; TriBench warms up for 200 ms by default)")
     ap.add_argument("--copy-probe-gib", type=float, default=0.0,
                     help="first run one plain device copy of this many GiB (calibrates rocprofv3 "
                          "FETCH_SIZE / WRITE_SIZE against a known byte count)")
@@ -166,7 +167,7 @@ def main(argv=None) -> int:
     copy_gbps = copy_rate_gbps()
     R = _load("reference")
     H = _load("hip_impl")
-    head = measure(R, H, args.config, args.steps, args.warmup, args.q_quant)
+    head = measure(R, H, args.config, args.steps, args.warmup, args.q_quant, args.settle_ms)
     _with_copy_rate(head, copy_gbps)
     case = CONFIGS[args.config]
     res = {
@@ -183,11 +184,12 @@ def main(argv=None) -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": head["config"],
-        **{key: head[key] for key in ("pct_int8_peak", "algo_tops", "latency_ms", "prepass", "roofline")},
+        **{key: head[key] for key in ("pct_int8_peak", "algo_tops", "algo_pct_int8_peak", "latency_ms", "settle",
+                                       "prepass", "roofline")},
     }
     if args.also != "none" and args.also != args.config:
         # the metric's N = 16384 half: the same measurement on configuration 3
-        other = measure(R, H, args.also, args.steps, args.warmup, args.q_quant)
+        other = measure(R, H, args.also, args.steps, args.warmup, args.q_quant, args.settle_ms)
         _with_copy_rate(other, copy_gbps)
         res[f"n{CONFIGS[args.also]['seq_len']}"] = other
     if not args.no_cpu_baseline:
@@ -225,12 +227,13 @@ def _with_copy_rate(res: dict, copy_gbps: float) -> None:
     pre["frac_of_copy"] = round(pre["gbps"] / copy_gbps, 4)
 
 
-def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
-    """``warmup`` untimed and ``steps`` timed forwards of configuration
-    ``name`` with its inputs resident in HBM: step time (one pair of events
-    around all steps), effective TOPS (the metric) and algorithmic TOPS,
-    p50/p95 of per-step events, the pre-pass's HBM rate, and the attention
-    kernel's roofline from events around its launches on its stream."""
+def measure(R, H, name: str, steps: int, warmup: int, q_quant: str, settle_ms: float = 0.0) -> dict:
+    """Untimed steps for ``settle_ms`` of wall time, ``warmup`` untimed and
+    ``steps`` timed forwards of configuration ``name`` with its inputs
+    resident in HBM: step time (one pair of events around all steps),
+    effective TOPS (the metric) and algorithmic TOPS, p50/p95 of per-step
+    events, the pre-pass's HBM rate, and the attention kernel's roofline from
+    events around its launches on its stream."""
     case = CONFIGS[name]
     dev = torch.device("cuda:0")
     inp = R.make_inputs(case, "cpu", 0, torch.bfloat16)
@@ -260,6 +263,16 @@ def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
         if ev is not None:
             ev[2].record(stream)
 
+    # the clock's ramp from idle: steps in groups of 4, the host kept within a
+    # group of the GPU, until settle_ms of wall time have passed
+    torch.cuda.synchronize()
+    n_settle, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(4):
+            step()
+        n_settle += 4
+        torch.cuda.synchronize()
+    settle_wall_ms = (time.perf_counter() - t0) * 1e3
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -280,6 +293,7 @@ def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
     torch.cuda.empty_cache()
 
     value = metric_ops / (ms * 1e-3) / 1e12
+    traffic, traffic_src = _traffic_from_profiles(name)
     # Q (unless the attention kernel quantizes it) and K quantization + V tiles
     pre_bytes = est["prepass_bytes_k" if fused_q else "prepass_bytes"] + est["vtile_bytes"]
     pre_gbps = pre_bytes / (float(pre_ms.mean()) * 1e-3) / 1e9
@@ -293,13 +307,18 @@ def measure(R, H, name: str, steps: int, warmup: int, q_quant: str) -> dict:
         "ms_per_step": round(ms, 4),
         "pct_int8_peak": round(100.0 * value / INT8_PEAK_TOPS, 2),
         "algo_tops": round(algo_ops / (ms * 1e-3) / 1e12, 2),
+        "algo_pct_int8_peak": round(100.0 * algo_ops / (ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 2),
+        **({"note": "causal: value and pct_int8_peak follow the metric's 4*B*H*N^2*D, which counts the "
+                    "masked pairs; algo_tops and algo_pct_int8_peak count the unmasked pairs only"}
+           if causal else {}),
         "latency_ms": {"p50": round(float(np.percentile(step_ms, 50)), 4),
                        "p95": round(float(np.percentile(step_ms, 95)), 4)},
+        "settle": {"ms": round(settle_wall_ms, 1), "steps": n_settle},
         "prepass": {"ms": round(float(pre_ms.mean()), 4), "bytes": pre_bytes, "gbps": round(pre_gbps, 1),
                     "hbm_frac": round(pre_gbps / HBM_PEAK_GBPS, 4)},
         "roofline": {"kernel": "attn_fwd_kernel", "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s", "frac": round(achieved / INT8_PEAK_TOPS, 4),
-                     "traffic": _traffic_from_profiles(name),
+                     "traffic": traffic, "traffic_source": traffic_src,
                      "launch_ms": round(float(attn_ms.mean()), 4), "algo_ops_per_launch": algo_ops},
     }
 

@@ -19,7 +19,6 @@ rate against 8 TB/s.
 from __future__ import annotations
 
 import os
-import platform
 import time
 from typing import Callable
 
@@ -104,16 +103,9 @@ def cpu_info() -> tuple[int, str]:
         threads = len(os.sched_getaffinity(0))
     except AttributeError:
         threads = os.cpu_count() or 1
-    model = platform.processor() or ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return threads, model
+    from .env import cpu_model
+
+    return threads, cpu_model()
 
 
 def run_benchmark(

@@ -15,6 +15,29 @@ def _git(args: list[str]) -> str:
         return ""
 
 
+def cpu_model() -> str:
+    """The host CPU as /proc/cpuinfo names it: the model name string in full,
+    with its family / model / stepping numbers (a virtualised host may give a
+    short model name), or the platform's processor string."""
+    fields: dict[str, str] = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    break  # the first processor's block is enough
+                key, _, val = line.partition(":")
+                fields[key.strip()] = val.strip()
+    except OSError:
+        pass
+    name = fields.get("model name")
+    if not name:
+        import platform
+
+        return platform.processor() or "unknown"
+    ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+    return f"{name} ({', '.join(ids)})" if ids else name
+
+
 def capture_env(cmdline: str = "") -> EnvInfo:
     import torch
 
@@ -33,14 +56,7 @@ def capture_env(cmdline: str = "") -> EnvInfo:
         env.cpu_threads = len(os.sched_getaffinity(0))
     except AttributeError:
         env.cpu_threads = os.cpu_count() or 0
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    env.cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    env.cpu_model = cpu_model()
     env.git_commit = _git(["rev-parse", "HEAD"])
     env.git_dirty = bool(_git(["status", "--porcelain"]))
     return env
