@@ -4,10 +4,13 @@ Every ``csrc/*.hip`` translation unit is compiled with ``hipcc
 --offload-arch=gfx950`` and linked into one shared library.  Builds in-tree
 (the ``.so`` travels with the source tree) and always recompiles.
 
-Usage: ``python -m tribench_amd.build [-j N] [--peak]``.  ``--peak`` also
-builds the roofline measurement programs of ``tribench_amd/peak`` (MFMA and
-HBM peaks); the library and the device checks the GPU tests run are always
-built.
+Usage: ``python -m tribench_amd.build [-j N] [--peak] [--trace]``.
+``--peak`` also builds the roofline measurement programs of
+``tribench_amd/peak`` (MFMA and HBM peaks); ``--trace`` also builds
+``lib/libsage_attn_trace.so``, the same sources with the attention kernel's
+phase trace compiled in (SAGE_TRACE=2, include/sage_trace.h), for
+``tribench_amd/trace_phases.py``.  The library and the device checks the GPU
+tests run are always built.
 """
 from __future__ import annotations
 
@@ -23,6 +26,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libsage_attn.so"
+TRACE_LIB = LIBDIR / "libsage_attn_trace.so"
 ARCH = "gfx950"
 
 # Common flags.  Packed-FP32 instructions are disabled for all device code.
@@ -56,8 +60,8 @@ def hipcc() -> str:
     return exe
 
 
-def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *COMMON, *UNIT_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, obj: Path, extra: tuple[str, ...] = ()) -> None:
+    cmd = [hipcc(), *COMMON, *UNIT_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
@@ -68,32 +72,40 @@ def _compile(src: Path, obj: Path) -> None:
         print("\n".join(msgs), file=sys.stderr)
 
 
-def build(jobs: int | None = None, verbose: bool = True, peak: bool = False) -> Path:
-    """Compile every HIP unit for gfx950 and link ``libsage_attn.so``, then
-    the device checks of ``tests/native`` (and, with ``peak``, the roofline
-    measurement programs)."""
+def _build_lib(out: Path, objdir: Path, jobs: int | None, extra: tuple[str, ...] = ()) -> Path:
     srcs = sorted(CSRC.glob("*.hip"))
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     objs = [objdir / (s.stem + ".o") for s in srcs]
     jobs = jobs or min(len(srcs), os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        for f in [ex.submit(_compile, s, o) for s, o in zip(srcs, objs)]:
+        for f in [ex.submit(_compile, s, o, extra) for s, o in zip(srcs, objs)]:
             f.result()
-    tmp = LIB.with_suffix(".so.tmp")
+    tmp = out.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, out)
+    return out
+
+
+def build(jobs: int | None = None, verbose: bool = True, peak: bool = False, trace: bool = False) -> Path:
+    """Compile every HIP unit for gfx950 and link ``libsage_attn.so``, then
+    the device checks of ``tests/native`` (and, with ``peak``, the roofline
+    measurement programs; with ``trace``, the phase-trace library)."""
+    _build_lib(LIB, PKG / "_build", jobs)
     if verbose:
         print(f"built {LIB}")
     build_checks(verbose)
     if peak:
         build_peak(verbose)
+    if trace:
+        _build_lib(TRACE_LIB, PKG / "_build" / "trace", jobs, ("-DSAGE_TRACE=2",))
+        if verbose:
+            print(f"built {TRACE_LIB}")
     return LIB
 
 
@@ -137,8 +149,9 @@ def main(argv: list[str] | None = None) -> int:
     p = argparse.ArgumentParser(description=__doc__)
     p.add_argument("-j", "--jobs", type=int, default=None)
     p.add_argument("--peak", action="store_true", help="also build the roofline measurement programs")
+    p.add_argument("--trace", action="store_true", help="also build the phase-trace library")
     args = p.parse_args(argv)
-    build(args.jobs, peak=args.peak)
+    build(args.jobs, peak=args.peak, trace=args.trace)
     return 0
 
 

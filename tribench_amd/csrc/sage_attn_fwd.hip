@@ -50,6 +50,13 @@
 
 #include "sage_device.h"
 
+// SAGE_TRACE (a measurement build only, libsage_attn_trace.so): every wave
+// records s_memtime at its phase boundaries and the cycles it spends at the
+// per-iteration barrier into a buffer attached with sage_trace_attach().
+#ifndef SAGE_TRACE
+#define SAGE_TRACE 0
+#endif
+
 namespace sage {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
@@ -74,7 +81,30 @@ struct AttnArgs {
   float q_mul;            // Q quantized here: its multiplier, fp32(sm_scale * 1.44269504)
   int8_t* q8_out;         // Q quantized here: optional copies of Q8 (q's strides) and q_scale
   float* qs_out;
+#if SAGE_TRACE
+  unsigned long long* trace;  // kTraceWords per wave, indexed by (blockIdx.x, wave)
+#endif
 };
+
+#if SAGE_TRACE
+// Words per wave of the phase trace: s_memtime at entry, end of the prologue
+// (before iteration 0), after iteration 0, after the mask-free loops, after
+// the generic iterations and after the epilogue's stores [0..5]; barrier wait
+// cycles over all iterations [6] and in the mask-free loops [7]; barrier
+// counts, all and mask-free [8]; s_memrealtime (100 MHz) at entry and exit
+// [9, 10]; HW_ID and XCC_ID [11]; the work-group's remapped index [12];
+// s_memtime after the prologue's Q quantization (its Q rows awaited) and
+// after its tile wait [13, 14].
+constexpr int kTraceWords = 16;
+
+// the stamps' LDS (a function-scope array: only the kernels that call this
+// allocate it)
+template <int NW>
+__device__ __forceinline__ unsigned long long* trace_lds() {
+  __shared__ unsigned long long s[NW * kTraceWords];
+  return s;
+}
+#endif
 
 // Operand type of the QK product: INT8 with per-block scales (SageAttention;
 // Q quantized by the pre-pass, or here from Q in the output type), or
@@ -238,6 +268,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   constexpr int SINK = LPW * NW > KLD + VLD ? 1024 : 0;  // target of spare loads
 
   __shared__ __attribute__((aligned(1024))) char smem[NBUF * SLOT + SINK];
+#if SAGE_TRACE
+  // stamps go to LDS as they are taken (kept in registers they would change
+  // the kernel being measured; a global store would enter the vmcnt
+  // accounting of the tile loads) and to the trace buffer at the end.  A
+  // kernel whose tile ring leaves no room for them is not traced.
+  constexpr bool kTrace = NBUF * SLOT + SINK + NW * kTraceWords * 8 <= 160 * 1024;
+  unsigned long long* tr_s = nullptr;
+  if constexpr (kTrace) tr_s = trace_lds<NW>();
+  // every lane stores the same wave-uniform value (no branch around the store)
+  auto tr_put = [&](int i, unsigned long long v) __attribute__((always_inline)) {
+    if constexpr (kTrace) tr_s[__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * kTraceWords + i] = v;
+  };
+  tr_put(0, __builtin_amdgcn_s_memtime());
+  tr_put(9, __builtin_amdgcn_s_memrealtime());
+  uint32_t tr_wait = 0, tr_wait_fast = 0, tr_n = 0;  // barrier cycles; counts (mask-free << 16)
+#endif
 
   const int nqb = (a.Nq + BM - 1) / BM;
   const int wg = remap_xcd((int)blockIdx.x, (int)gridDim.x);
@@ -389,11 +435,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   };
   // end of an iteration: this wave's loads of the tile needed next are done
   // (at most `ahead` younger tiles in flight), its LDS reads are done, barrier
-  auto sync_tiles = [&](bool ahead) __attribute__((always_inline)) {
+  // (fast: called from the mask-free loops, for the trace's split)
+  auto sync_tiles = [&](bool ahead, bool fast = false) __attribute__((always_inline)) {
     if (ahead) SAGE_WAIT_VM(LPW);
     else SAGE_WAIT_VM(0);
+#if SAGE_TRACE >= 2
+    const unsigned long long tb = __builtin_amdgcn_s_memtime();
+#endif
     SAGE_WAIT_LGKM0();
     wg_barrier();
+#if SAGE_TRACE >= 2
+    const uint32_t dt = (uint32_t)(__builtin_amdgcn_s_memtime() - tb);
+    tr_wait += dt;
+    tr_n += fast ? 0x10001u : 1u;
+    if (fast) tr_wait_fast += dt;
+#endif
   };
 
   // ---- INT8 scores in one FMA, rounded once.  With the accumulator read as
@@ -708,7 +764,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     else softmax(j, Pcur, false);
     keep_p();
     qk(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF);
-    sync_tiles(true);
+    sync_tiles(true, true);
   };
 
   // INT8 with fp16 P, and fp16/bf16 QK at D = 64: the S of block j+1 goes to
@@ -738,7 +794,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     qk_into(j + 1, sl < 0 ? (j + 1) % NBUF : (sl + 1) % NBUF, Sb, kb);
     softmax_fast_on(j, Pcur, Sa, ka);
     keep_p();
-    sync_tiles(true);
+    sync_tiles(true, true);
   };
 
   // Q quantization (kFQ) with the pre-pass's arithmetic (per_block_int8,
@@ -816,7 +872,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   load_tile(min(1, nkb - 1), min(1, nkb - 1));
   load_tile(min(2, nkb - 1), min(2, nkb - 1));
   quantize_q();
+#if SAGE_TRACE
+  tr_put(13, __builtin_amdgcn_s_memtime());
+#endif
   sync_tiles(nkb > 2);
+#if SAGE_TRACE
+  tr_put(14, __builtin_amdgcn_s_memtime());
+#endif
   if (jmax >= 0) qk(0, 0);
 
   if constexpr (kI8) {  // mgrid = 4 ulp(kMagicF * c_max): exponent field of that product - 21,
@@ -829,7 +891,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     mgrid_inv = __uint_as_float((uint32_t)(254 - eg) << 23);
   }
   const int j_fast = min(min(nfull, jmax), min(nkb, a.Nkv / kBN) - 3);  // tile j+3 whole
+#if SAGE_TRACE
+  tr_put(1, __builtin_amdgcn_s_memtime());
+#endif
   generic_iter(0);
+#if SAGE_TRACE
+  tr_put(2, __builtin_amdgcn_s_memtime());
+#endif
   int j = 1;
   // D = 64 (INT8 with fp16 P, and fp16/bf16 QK): constant ring slots, j % NBUF
   // == 1 at every trip (at D = 128 the copies run out of registers); then
@@ -861,7 +929,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
       fused_iter(j + 1, -1, S2, ksc2, S, ksc_cur);
     }
   for (; j < j_fast; ++j) fast_iter(j, -1);
+#if SAGE_TRACE
+  tr_put(3, __builtin_amdgcn_s_memtime());
+#endif
   for (; j <= nkb; ++j) generic_iter(j);
+#if SAGE_TRACE
+  tr_put(4, __builtin_amdgcn_s_memtime());
+#endif
 
   // ---- epilogue: O / l, store row q = qa + n, d = 32dt + 8i + 4hh .. +4
   if (pend) rescale_o();
@@ -907,14 +981,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
       for (int i = 0; i < 4; ++i) out4(dt, i, obase + (uint32_t)(row * a.son));
   }
+#if SAGE_TRACE
+  tr_put(5, __builtin_amdgcn_s_memtime());
+  tr_put(10, __builtin_amdgcn_s_memrealtime());
+  tr_put(6, tr_wait);
+  tr_put(7, tr_wait_fast);
+  tr_put(8, (unsigned long long)(tr_n & 0xFFFF) | ((unsigned long long)(tr_n >> 16) << 32));
+  tr_put(11, (unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 4) |
+                 ((unsigned long long)__builtin_amdgcn_s_getreg((31 << 11) | 20) << 32));
+  tr_put(12, (unsigned long long)wg);
+  if constexpr (kTrace) {
+    SAGE_WAIT_LGKM0();
+    if (a.trace && lane < kTraceWords)
+      a.trace[((size_t)blockIdx.x * NW + wave) * kTraceWords + lane] = tr_s[wave * kTraceWords + lane];
+  }
+#endif
 }
+
+#if SAGE_TRACE
+static unsigned long long* g_trace = nullptr;
+static int64_t g_trace_words = 0;
+#endif
 
 template <int QKM, int D, int PVM, typename TO>
 static int launch_cfg(const AttnArgs& a, hipStream_t st, const char* who) {
   const int64_t nqb = (a.Nq + 255) / 256;
   const int64_t grid = nqb * a.Hq * a.B;
   if (grid > 0x7FFFFFFF) return fail("%s: invalid argument: grid too large", who);
+#if SAGE_TRACE
+  AttnArgs at = a;
+  at.trace = g_trace;
+  if (g_trace && grid * 8 * kTraceWords > g_trace_words)
+    return fail("%s: invalid argument: trace buffer of %lld words < %lld", who, (long long)g_trace_words,
+                (long long)(grid * 8 * kTraceWords));
+  hipLaunchKernelGGL((attn_fwd_kernel<QKM, D, PVM, TO>), dim3((unsigned)grid), dim3(512), 0, st, at);
+#else
   hipLaunchKernelGGL((attn_fwd_kernel<QKM, D, PVM, TO>), dim3((unsigned)grid), dim3(512), 0, st, a);
+#endif
   return check_launch(who);
 }
 
@@ -1084,6 +1187,18 @@ extern "C" int sage_attn_fwd_q(const void* q, const int64_t* q_strides, int q_dt
     default: return launch_pv_q<__bf16>(a, d, pv_mode, st);
   }
 }
+
+#if SAGE_TRACE
+// Measurement build only (include/sage_trace.h): the attention launches that
+// follow write their phase trace into buf (at least grid * 8 * 16 words), or
+// into nothing again after a call with buf = NULL.
+extern "C" int sage_trace_attach(unsigned long long* buf, int64_t words) {
+  if (buf && words <= 0) return fail("sage_trace_attach: invalid argument: words %lld", (long long)words);
+  g_trace = buf;
+  g_trace_words = buf ? words : 0;
+  return 0;
+}
+#endif
 
 extern "C" int sage_flash_fwd(const void* q, const int64_t* q_strides, const void* k, const int64_t* k_strides,
                               const void* v, int v_dtype, const int64_t* v_strides, void* o,
