@@ -153,6 +153,7 @@ def main(argv=None) -> int:
     ap.add_argument("--dtype", default="bf16", choices=["bf16", "fp16"])
     ap.add_argument("--settle-ms", type=float, default=300.0)
     ap.add_argument("--compare", type=int, default=20, help="alternating timed launches of each library")
+    ap.add_argument("--save", default=None, help="also write the raw trace [grid, 8, 16] to this .npy file")
     args = ap.parse_args(argv)
     import torch
 
@@ -200,6 +201,8 @@ def main(argv=None) -> int:
     T = buf.cpu().numpy().view(np.uint64).reshape(grid, NW, WORDS)
     if not (T[:, :, 5] > 0).all():
         raise SystemExit("trace incomplete: some waves wrote no record")
+    if args.save:
+        np.save(args.save, T)
     print(f"### {name} ({args.dtype}, {'causal' if causal else 'non-causal'}, {opts or 'defaults'})\n")
     print(f"forward (pre-pass + attention), median of {args.compare} alternating: product "
           f"{np.median(ms['product']):.4f} ms, trace build {np.median(ms['trace']):.4f} ms\n")
