@@ -67,3 +67,17 @@ def test_analyse_synthetic_trace():
     assert "entry to Q quantized (Q rows awaited) 15000" in out
     assert "the wave that issues ahead 3.1 %, the other 15.6 %" in out
     assert "gap between consecutive work-groups on one CU 2.00 us median (256 CUs seen)" in out
+
+
+def test_dispatch_replay_by_hand():
+    """In-order dispatch to engines in turn, one CU per engine: the long first
+    work-group holds back the second round on every engine."""
+    n = 8  # work-groups of XCD 0: blockIdx 0, 8, 16, ...
+    T = np.zeros((8 * n, tp.NW, tp.WORDS), dtype=np.uint64)
+    durs = [4, 1, 1, 1, 1, 1, 1, 1]
+    for i, d in enumerate(durs):
+        g = 8 * i
+        T[g, :, 9], T[g, :, 10] = 0, d * 100
+        T[g, :, 11] = (i % 4) << 13
+    sim, meas, idle = tp.simulate_dispatch(T, xcd=0, cus_per_engine=1)
+    assert abs(sim - 5.25) < 1e-9 and meas == 4.0 and abs(idle - 9.7 / 4) < 1e-9
