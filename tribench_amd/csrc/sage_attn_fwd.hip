@@ -504,6 +504,15 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   for (int dt = 0; dt < DT; ++dt) oacc[dt] = (v16f){};
   float m_use = -INFINITY;
   float lsum = 0.0f;     // this lane's share of the row sum
+  // FP8 P: the row sums come from the matrix pipe, one more P.V MFMA per
+  // block with an all-ones A operand (e4m3 1.0 = 0x38): every row of osum is
+  // the sum of the block's e4m3 P, accumulated in fp32 and rescaled with O.
+  // It replaces 32 fp32 additions per lane and block on the VALU, which sets
+  // the FP8 loop's pace, and sums exactly the P the P.V product uses.
+  constexpr bool kSumMfma = kF8;
+  v16f osum = (v16f){};
+  v8i ones8 = {0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838, 0x38383838};
+  if constexpr (kSumMfma) asm volatile("" : "+v"(ones8));
   float alpha_o = 1.0f;  // pending factor of O
   bool pend = false;     // O must be multiplied by alpha_o before the next P.V
   SAcc S[2];             // S^T of key tiles 0 and 1 of the block in flight
@@ -564,6 +573,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         const v8i va = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
         const v8i pb = {(int)P[0], (int)P[1], (int)P[2], (int)P[3], (int)P[4], (int)P[5], (int)P[6], (int)P[7]};
         oacc[dt] = Pv::mma(va, pb, oacc[dt]);
+        if constexpr (kSumMfma)
+          if (dt == DT - 1) osum = Pv::mma(ones8, pb, osum);
       } else {
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {  // 16-key steps: key tile kk/2, register half kk%2
@@ -659,7 +670,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int w = 0; w < 8; ++w) P[8 * t + w] = Pv::pack2(p[2 * w], p[2 * w + 1]);
       }
-      if constexpr (!kSumF16) {
+      if constexpr (!kSumF16 && !kSumMfma) {
 #pragma unroll
         for (int w = 8; w >= 1; w >>= 1)
 #pragma unroll
@@ -676,7 +687,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 #pragma unroll
         for (int i = 0; i < w; ++i) hs[i] = hs[i] + hs[i + w];
       lsum = __builtin_amdgcn_fdot2(hs[0], (h2){(_Float16)1.0f, (_Float16)1.0f}, lsum, false);
-    } else {
+    } else if constexpr (!kSumMfma) {
       lsum += ls[0] + ls[1];
     }
   };
@@ -748,6 +759,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   auto rescale_o = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) oacc[dt] *= alpha_o;
+    if constexpr (kSumMfma) osum *= alpha_o;
     alpha_o = 1.0f;
   };
   auto keep_p = [&]() __attribute__((always_inline)) {
@@ -970,7 +982,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   if (pend) rescale_o();
   TO* obase = static_cast<TO*>(a.o) + b * a.so[0] + h * a.so[1];
   const float* vsc = kF8 ? a.v_scale + ((int64_t)b * a.Hkv + hk) * D : nullptr;
-  const float inv = 1.0f / sum_halves(lsum);
+  const float inv = 1.0f / (kSumMfma ? osum[0] : sum_halves(lsum));
   const int row = qa + n;
   auto out4 = [&](int dt, int i, TO* p) __attribute__((always_inline)) {
     const int d0 = 32 * dt + 8 * i + 4 * hh;
