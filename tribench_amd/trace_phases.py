@@ -46,15 +46,25 @@ NW = 8      # waves per work-group
 
 
 def _load(stem: str, lib: Path):
-    """The pack file ``stem`` under a module name of its own, bound to ``lib``."""
-    os.environ["TRIBENCH_SAGE_HIP_LIB"] = str(lib)
+    """The pack file ``stem`` under a module name of its own, bound to ``lib``
+    (the library override variable is set only while it binds)."""
     name = f"tribench.kernels.sage_attn.{stem}.{lib.stem}"
+    if name in sys.modules:
+        return sys.modules[name]
     spec = importlib.util.spec_from_file_location(name, PACK / f"{stem}.py")
     mod = importlib.util.module_from_spec(spec)
     sys.modules[name] = mod
     spec.loader.exec_module(mod)
     if hasattr(mod, "_load"):
-        mod._load()  # bind now, while the variable names this library
+        old = os.environ.get("TRIBENCH_SAGE_HIP_LIB")
+        os.environ["TRIBENCH_SAGE_HIP_LIB"] = str(lib)
+        try:
+            mod._load()  # bind now, while the variable names this library
+        finally:
+            if old is None:
+                del os.environ["TRIBENCH_SAGE_HIP_LIB"]
+            else:
+                os.environ["TRIBENCH_SAGE_HIP_LIB"] = old
     return mod
 
 
